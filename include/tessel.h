@@ -1,0 +1,155 @@
+/*
+ * tessel_amd: the C ABI of the MI355X (gfx950) kernel library.
+ *
+ * One device, one stream, driven from one thread at a time: the launch
+ * surface of tessel's GPU layer (src/gpu.rs, src/runtime.rs, src/driver.rs),
+ * with hand-written HIP kernels behind the same kernel names and argument
+ * order as the .tl sources (kernels/{basic,matmul,attention,llm}.tl).
+ *
+ * Every call returns 0 on success or a negative status; tsl_last_error()
+ * then gives the message ("{what}: HIP error {code} {name}" for HIP
+ * failures, as src/driver.rs:181-195 formats CUDA ones). Plain pointers and
+ * sizes only: device pointers travel as uint64_t.
+ */
+#ifndef TESSEL_H
+#define TESSEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSL_OK 0
+#define TSL_ERR_HIP (-1)     /* a HIP call failed */
+#define TSL_ERR_ARG (-2)     /* bad argument: arity, shape, meta, bounds */
+#define TSL_ERR_NOKERNEL (-3) /* no such file/kernel */
+
+/* The message of the last failed call on this thread ("" if none). */
+const char* tsl_last_error(void);
+
+/* ---- device (src/driver.rs:110-179 Cuda::open/bind; src/runtime.rs:48-52) */
+
+/* Opens device 0 and creates the library's stream (idempotent). */
+int tsl_open(void);
+/* Device name (gcnArchName + marketing name) into buf. */
+int tsl_device_name(char* buf, size_t len);
+/* Compute units and peak clock in MHz, for roofline figures. */
+int tsl_device_info(int* cus, int* mhz);
+/* Waits for the stream (src/driver.rs:274-277 Cuda::sync). */
+int tsl_sync(void);
+/* The library's stream, as a hipStream_t cast to a pointer. */
+void* tsl_stream(void);
+
+/* ---- memory (src/gpu.rs:70-133, src/driver.rs:197-272) */
+
+/* A zero-filled device buffer of at least max(bytes, 4) bytes. */
+int tsl_alloc(size_t bytes, uint64_t* dptr);
+/* Frees a buffer from tsl_alloc (the reference never frees; added). */
+int tsl_free(uint64_t dptr);
+/* Synchronous host->device copy of n bytes (src/driver.rs:245-254). */
+int tsl_upload(uint64_t dst, const void* src, size_t n);
+/* Synchronous device->host copy of n bytes, after the stream drains
+ * (src/gpu.rs:110-133, src/driver.rs:256-264). */
+int tsl_download(void* dst, uint64_t src, size_t n);
+/* Fills n 32-bit words with a quiet NaN (src/driver.rs:266-272). */
+int tsl_fill_nan(uint64_t dst, size_t n);
+
+/* ---- kernels (src/gpu.rs:148-216 Gpu::kernel / Gpu::launch,
+ *                src/runtime.rs:202-236 Compiled::launch_raw) */
+
+/*
+ * Kernel `name` of file `file` ("basic", "matmul", "attention", "llm"),
+ * specialised for the array shapes given in parameter order: nshapes
+ * arrays, array i has ranks[i] dimensions stored consecutively in dims.
+ * meta_names/meta_values override the kernel's meta constants (an unknown
+ * name is an error, src/ir.rs:1039-1043); warps is recorded in the key.
+ * The same key "{file}/{name} {shapes:?} {meta:?} {warps}"
+ * (src/gpu.rs:156) returns the same handle.
+ */
+int tsl_kernel(const char* file, const char* name, int nshapes, const int* ranks, const int64_t* dims,
+               int nmeta, const char* const* meta_names, const int64_t* meta_values, int warps,
+               int* handle);
+/* The cache key of a handle, into buf. */
+int tsl_kernel_key(int handle, char* buf, size_t len);
+/*
+ * Launches kernel `handle` asynchronously on the library stream with one
+ * 64-bit argument per .tl parameter, in declaration order: arrays are
+ * device pointers, f32/i32 scalars their bit pattern in the low 32 bits
+ * (src/gpu.rs:179-195). An arity mismatch is an error (src/runtime.rs:203).
+ */
+int tsl_launch(int handle, const uint64_t* args, int nargs);
+
+/* ---- timing and graphs (src/driver.rs:340-380, src/runtime.rs:295-316) */
+
+/* Event-timed milliseconds of `iters` launches of handle (after the stream
+ * drains); ms receives the total. */
+int tsl_time_launches(int handle, const uint64_t* args, int nargs, int iters, float* ms);
+/* Starts recording this thread's launches on the stream into a graph
+ * (relaxed capture mode, src/driver.rs:340-348). */
+int tsl_capture_begin(void);
+/* Ends the recording and instantiates it: *graph identifies it. */
+int tsl_capture_end(int* graph);
+/* Replays a recorded graph asynchronously (src/driver.rs:360-363). */
+int tsl_replay(int graph);
+/* Events on the stream, for timing a caller's own sequence. */
+int tsl_event_record(int* event);
+int tsl_event_elapsed(int start, int end, float* ms);
+
+/* ---- the LLM engine (src/llm/engine.rs, src/llm/sched.rs, src/llm/mod.rs) */
+
+/* Config (src/llm/mod.rs:15-28). */
+typedef struct {
+    int32_t dim, layers, heads, kv_heads, head_dim, ffn, vocab;
+    float eps, rope_theta;
+    int32_t max_pos, bos, eos;
+} tsl_config;
+
+/* Limits (src/llm/engine.rs:23-32). */
+typedef struct {
+    int32_t page, pages, max_tokens, max_seq_pages;
+} tsl_limits;
+
+/* Weights::random(cfg, seed) (src/llm/mod.rs:80-108) into host arrays of
+ * f16 bits: embed[vocab*dim], per layer (attn_norm[dim],
+ * wqkv[(H+2G)*D*dim], wo[dim*H*D], mlp_norm[dim], wg[ffn*dim],
+ * wu[ffn*dim], wd[dim*ffn]) concatenated layer after layer, norm[dim],
+ * lm_head[vocab*dim]. Sizes from tsl_weights_sizes. */
+int tsl_weights_sizes(const tsl_config* cfg, size_t* embed, size_t* per_layer, size_t* norm, size_t* head);
+int tsl_weights_random(const tsl_config* cfg, uint64_t seed, uint16_t* embed, uint16_t* layers, uint16_t* norm,
+                       uint16_t* head);
+
+/* Engine::new (src/llm/engine.rs:150-223): uploads the weights (layout as
+ * tsl_weights_random; head may be NULL to tie it to embed). */
+int tsl_engine_new(const tsl_config* cfg, const tsl_limits* lim, const uint16_t* embed, const uint16_t* layers,
+                   const uint16_t* norm, const uint16_t* head, int* engine);
+int tsl_engine_free(int engine);
+/* Engine flags: graphs (decode-step graph replay), tune (matmul tuner). */
+int tsl_engine_set(int engine, int graphs, int tune);
+
+/* Engine::step (src/llm/engine.rs:275-354). mode 0 = Prefill, 1 = Packed
+ * (starts[n]), 2 = Decode (tables: nseq rows of max_seq_pages pages, lens:
+ * nseq). logits receives nwant * vocab floats for rows want[0..nwant). */
+int tsl_engine_step(int engine, int n, const int32_t* tokens, const int32_t* pos, const int32_t* slots, int mode,
+                    const int32_t* starts, int nseq, const int32_t* tables, const int32_t* lens, int nwant,
+                    const int32_t* want, float* logits);
+
+/* sched::generate_with (src/llm/sched.rs:52-179): greedy generation of
+ * nreq requests (prompt r = prompts[offsets[r] .. offsets[r+1]), max_new[r]
+ * tokens). out_tokens gets sum(max_new) slots: request r's tokens start at
+ * the prefix sum of max_new; out_counts[r] is how many it produced.
+ * stats: prefill_steps, decode_steps, prompt_tokens, generated,
+ * largest_batch, decode_tokens (int64) and seconds, decode_seconds. */
+typedef struct {
+    int64_t prefill_steps, decode_steps, prompt_tokens, generated, largest_batch, decode_tokens;
+    double seconds, decode_seconds;
+} tsl_stats;
+int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* offsets, const int32_t* max_new,
+                 int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,59 @@
+"""Builds tessel_amd/libtessel_hip.so: the gfx950 kernels and the C ABI of
+include/tessel.h, compiled in-tree with hipcc (every source to an object in
+parallel, then one shared library)."""
+
+import concurrent.futures
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libtessel_hip.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("TSL_CXX", "/opt/rocm/llvm/bin/clang++")  # host C++ with _Float16
+ARCH = "gfx950"
+
+# Packed-FP32 instructions are disabled for every device pass: hipcc -O3 would
+# otherwise form them from plain float code.
+HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall"]
+
+SOURCES = ["runtime.hip", "gemm.hip", "attention.hip", "decode.hip", "rows.hip"]
+HOST_SOURCES = ["engine.cpp"]
+
+
+def _compile(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError("compile failed: " + " ".join(cmd) + "\n" + err)
+    return err
+
+
+def build(verbose=False):
+    os.makedirs(BUILD, exist_ok=True)
+    jobs = []
+    objs = []
+    for s in SOURCES:
+        o = os.path.join(BUILD, s.replace(".hip", ".o"))
+        objs.append(o)
+        jobs.append([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, s), "-o", o])
+    for s in HOST_SOURCES:
+        o = os.path.join(BUILD, s.replace(".cpp", ".o"))
+        objs.append(o)
+        jobs.append([CXX] + HOST_FLAGS + ["-c", os.path.join(CSRC, s), "-o", o])
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+        for err in ex.map(_compile, jobs):
+            if verbose and err.strip():
+                print(err, file=sys.stderr)
+    tmp = LIB + ".tmp"
+    _compile([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", tmp] + objs)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,100 @@
+// Shared device helpers for the gfx950 kernels: vector types, f16
+// conversions, 64-lane wavefront reductions and the kernel-handle type the
+// launchers receive.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+typedef _Float16 half_t;
+typedef half_t half8 __attribute__((ext_vector_type(8)));
+typedef half_t half4 __attribute__((ext_vector_type(4)));
+typedef half_t half2v __attribute__((ext_vector_type(2)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16;
+
+#define TSL_DEV __device__ __forceinline__
+
+// Reinterpreting one element of an ext_vector in place,
+// __builtin_bit_cast(T, v[i]), reads element 0 whatever i is with this
+// clang (checked on the host: {1, 2, 3, 4}[i] as float gives 1 for every i).
+// Elements are therefore always passed by value through these helpers.
+TSL_DEV half2v as_half2(uint32_t x) { return __builtin_bit_cast(half2v, x); }
+TSL_DEV float as_float(uint32_t x) { return __builtin_bit_cast(float, x); }
+
+// f16 bits <-> f32 (hardware conversions: round to nearest even).
+TSL_DEV float h2f(u16 h) { return (float)__builtin_bit_cast(half_t, h); }
+TSL_DEV u16 f2h(float f) { return __builtin_bit_cast(u16, (half_t)f); }
+
+// Largest / sum over the 64 lanes of a wavefront, every lane receiving it.
+TSL_DEV float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+TSL_DEV float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+// DPP row operations within 16-lane rows (gfx9 DPP controls).
+template <int CTRL>
+TSL_DEV float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+// quad_perm [1,0,3,2] (xor 1), quad_perm [2,3,0,1] (xor 2), row_half_mirror, row_mirror.
+#define DPP_XOR1 0xb1
+#define DPP_XOR2 0x4e
+#define DPP_HALF_MIRROR 0x141
+#define DPP_MIRROR 0x140
+// Sum over the 16 lanes of each row, every lane of the row receiving it.
+TSL_DEV float row16_sum(float x) {
+    x += dpp<DPP_XOR1>(x);
+    x += dpp<DPP_XOR2>(x);
+    x += dpp<DPP_HALF_MIRROR>(x);
+    x += dpp<DPP_MIRROR>(x);
+    return x;
+}
+
+// A kernel specialised by tsl_kernel: its resolved dimensions and meta
+// values, in the order the .tl signature names them.
+struct TslKernel {
+    std::string file, name, key;
+    std::vector<std::vector<int64_t>> shapes;          // array params, in order
+    std::vector<std::pair<std::string, int64_t>> meta;  // declared order, overrides applied
+    std::vector<std::pair<std::string, int64_t>> dims;  // symbolic dims -> values
+    int warps = 4;
+    int nparams = 0;
+    // Library-owned device scratch (allocated once per handle, outside any
+    // graph capture), e.g. split-context partials of decode attention.
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    int64_t dim(const char* n) const;
+    int64_t metav(const char* n) const;
+};
+
+typedef int (*tsl_launcher)(TslKernel& k, const uint64_t* args, hipStream_t s);
+typedef int (*tsl_preparer)(TslKernel& k);  // optional: scratch sizing at tsl_kernel time
+
+// Records an argument/launch error (the C ABI's last error).
+int tsl_fail(int code, const std::string& msg);
+int tsl_hip_check(hipError_t e, const char* what);
+
+template <class T>
+inline T* P(uint64_t a) { return reinterpret_cast<T*>(a); }
+inline float arg_f32(uint64_t a) {
+    uint32_t b = (uint32_t)a;
+    float f;
+    __builtin_memcpy(&f, &b, 4);
+    return f;
+}
+inline int32_t arg_i32(uint64_t a) { return (int32_t)(uint32_t)a; }
+
+// The launch check after a kernel launch (a bad configuration fails here).
+#define TSL_LAUNCHED(what) tsl_hip_check(hipGetLastError(), what)

@@ -1,0 +1,638 @@
+// The LLM engine on the C ABI: a Llama-family decoder whose GPU work is
+// only the llm.tl kernels, with a paged KV cache and continuous batching.
+//
+//   Config / Weights::random / rope_tables / argmax   src/llm/mod.rs:15-140
+//   Engine::new / mm (tuner) / step / launch_all      src/llm/engine.rs:150-529
+//   sched::generate_with                              src/llm/sched.rs:52-179
+//
+// Host code only: every kernel is reached through tsl_kernel/tsl_launch, so
+// the engine drives exactly the launch surface a Rust caller would.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <deque>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/tessel.h"
+
+int tsl_fail(int code, const std::string& msg);
+
+namespace {
+
+typedef uint16_t u16;
+
+// ---------------------------------------------------------------- src/llm/mod.rs
+
+struct Rng {  // src/bench.rs:13-35
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed * 0x9e3779b97f4a7c15ull | 1ull) {}
+    uint64_t bits() {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        return s;
+    }
+    float uniform() { return ((float)(bits() >> 40) / (float)(1ull << 24)) * 2.0f - 1.0f; }
+};
+
+u16 to_f16(float f) { return __builtin_bit_cast(u16, (_Float16)f); }  // round to nearest even
+float from_f16(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+int64_t qkv_rows(const tsl_config& c) { return (int64_t)(c.heads + 2 * c.kv_heads) * c.head_dim; }
+int64_t layer_elems(const tsl_config& c) {
+    int64_t d = c.dim, hd = (int64_t)c.heads * c.head_dim;
+    return d + qkv_rows(c) * d + d * hd + d + 2 * (int64_t)c.ffn * d + d * c.ffn;
+}
+
+void rope_tables(const tsl_config& c, std::vector<float>& cs, std::vector<float>& sn) {
+    int64_t h = c.head_dim / 2;
+    cs.resize((size_t)c.max_pos * h);
+    sn.resize(cs.size());
+    for (int64_t p = 0; p < c.max_pos; p++)
+        for (int64_t i = 0; i < h; i++) {
+            double inv = std::pow((double)c.rope_theta, -((double)(2 * i)) / (double)c.head_dim);
+            double a = (double)p * inv;
+            cs[p * h + i] = (float)std::cos(a);
+            sn[p * h + i] = (float)std::sin(a);
+        }
+}
+
+size_t argmax(const float* xs, size_t n) {
+    size_t best = 0;
+    for (size_t i = 0; i < n; i++)
+        if (xs[i] > xs[best]) best = i;
+    return best;
+}
+
+// ---------------------------------------------------------------- the engine
+
+struct Buf {
+    uint64_t p = 0;
+    size_t bytes = 0;
+};
+
+struct Layer {
+    Buf n1, wqkv, wo, n2, wg, wu, wd, kc, vc;
+};
+
+enum Mode { PREFILL = 0, PACKED = 1, DECODE = 2 };
+
+struct Arg {  // src/gpu.rs:22-26
+    enum { BUF, F32 } kind;
+    uint64_t v;
+};
+
+size_t padded(size_t n) {  // src/llm/engine.rs:96-98
+    size_t t = std::max<size_t>(n, 16), p = 1;
+    while (p < t) p <<= 1;
+    return p;
+}
+
+typedef std::vector<std::pair<std::string, int64_t>> Meta;
+
+// src/llm/engine.rs:106-147: the tile configurations tried for an m-row matmul.
+std::vector<std::pair<Meta, int>> mm_candidates(size_t m, bool two) {
+    auto c = [](int64_t bm, int64_t bn, int64_t bk, int w) {
+        return std::make_pair(Meta{{"BM", bm}, {"BN", bn}, {"BK", bk}}, w);
+    };
+    if (m >= 64) {
+        if (two) return {c(64, 64, 32, 4), c(128, 64, 32, 4), c(64, 32, 32, 4)};
+        return {c(64, 128, 32, 4), c(64, 64, 32, 4), c(128, 128, 32, 4), c(128, 64, 32, 4)};
+    }
+    if (m >= 32) {
+        std::vector<std::pair<Meta, int>> v = {c(32, 64, 64, 4),  c(32, 32, 64, 4), c(32, 32, 128, 4),
+                                               c(32, 64, 128, 4), c(32, 16, 128, 2), c(16, 64, 64, 4),
+                                               c(16, 32, 128, 4)};
+        if (!two) v.push_back(c(32, 16, 256, 2));
+        return v;
+    }
+    return {c(16, 64, 64, 4), c(16, 32, 64, 4), c(16, 32, 128, 4), c(16, 64, 128, 4), c(16, 16, 128, 2),
+            c(16, 16, 256, 2)};
+}
+
+#define TRY(x)             \
+    do {                   \
+        int _r = (x);      \
+        if (_r) return _r; \
+    } while (0)
+
+struct Engine {
+    tsl_config cfg;
+    tsl_limits lim;
+    bool graphs = true, tune = true;
+    std::map<size_t, int> graph;
+    std::map<std::string, int> tuned;
+    Buf embed, head, norm, cos, sin;
+    std::vector<Layer> layers;
+    Buf x, h, qkv, q, k, v, o, mlp, last, logits, tok, pos, slot, idx, table, lens, starts;
+
+    int alloc(size_t bytes, Buf& b) {
+        b.bytes = bytes;
+        return tsl_alloc(bytes, &b.p);
+    }
+    int write(const Buf& b, size_t off, const void* data, size_t n) {
+        if (off + n > b.bytes) {
+            std::ostringstream e;
+            e << "write of " << n << " bytes at " << off << " into a buffer of " << b.bytes;
+            return tsl_fail(TSL_ERR_ARG, e.str());
+        }
+        return tsl_upload(b.p + off, data, n);
+    }
+    int up16(const u16* v, size_t n, Buf& b) {
+        TRY(alloc(n * 2, b));
+        return write(b, 0, v, n * 2);
+    }
+
+    int kernel(const char* name, const std::vector<std::vector<int64_t>>& shapes, const Meta& meta, int warps,
+               int* handle) {
+        std::vector<int> ranks;
+        std::vector<int64_t> dims;
+        for (auto& s : shapes) {
+            ranks.push_back((int)s.size());
+            dims.insert(dims.end(), s.begin(), s.end());
+        }
+        std::vector<const char*> names;
+        std::vector<int64_t> vals;
+        for (auto& m : meta) {
+            names.push_back(m.first.c_str());
+            vals.push_back(m.second);
+        }
+        return tsl_kernel("llm", name, (int)shapes.size(), ranks.data(), dims.data(), (int)meta.size(), names.data(),
+                          vals.data(), warps, handle);
+    }
+
+    int launch(int k, const std::vector<Arg>& args) {
+        std::vector<uint64_t> raw;
+        for (auto& a : args) raw.push_back(a.v);
+        return tsl_launch(k, raw.data(), (int)raw.size());
+    }
+
+    // Engine::mm (src/llm/engine.rs:233-270): with tuning on, every
+    // candidate is timed (3 warm-up launches, then 10) on the engine's own
+    // buffers and the fastest kept.
+    int mm(const char* name, const std::vector<std::vector<int64_t>>& shapes, bool two, const std::vector<Arg>& args,
+           int* out) {
+        std::ostringstream key;
+        key << name << " [";
+        for (size_t i = 0; i < shapes.size(); i++) {
+            key << (i ? ", " : "") << "[";
+            for (size_t j = 0; j < shapes[i].size(); j++) key << (j ? ", " : "") << shapes[i][j];
+            key << "]";
+        }
+        key << "]";
+        auto it = tuned.find(key.str());
+        if (it != tuned.end()) {
+            *out = it->second;
+            return 0;
+        }
+        auto cands = mm_candidates((size_t)shapes[0][0], two);
+        int pick = -1;
+        if (!tune) {
+            TRY(kernel(name, shapes, cands[0].first, cands[0].second, &pick));
+        } else {
+            float best = 1e30f;
+            std::vector<uint64_t> raw;
+            for (auto& a : args) raw.push_back(a.v);
+            for (auto& c : cands) {
+                int k;
+                if (kernel(name, shapes, c.first, c.second, &k)) continue;
+                bool ok = true;
+                for (int i = 0; i < 3 && ok; i++) ok = tsl_launch(k, raw.data(), (int)raw.size()) == 0;
+                float ms = 0;
+                if (ok) ok = tsl_time_launches(k, raw.data(), (int)raw.size(), 10, &ms) == 0;
+                if (ok && ms < best) {
+                    best = ms;
+                    pick = k;
+                }
+            }
+            if (pick < 0) return tsl_fail(TSL_ERR_ARG, key.str() + ": no configuration ran");
+        }
+        tuned[key.str()] = pick;
+        *out = pick;
+        return 0;
+    }
+
+    int init(const tsl_config& c, const tsl_limits& l, const u16* w_embed, const u16* w_layers, const u16* w_norm,
+             const u16* w_head) {
+        cfg = c;
+        lim = l;
+        if (cfg.kv_heads <= 0 || cfg.heads % cfg.kv_heads != 0 || cfg.head_dim % 2 != 0)
+            return tsl_fail(TSL_ERR_ARG, "heads must be a multiple of kv_heads, head_dim even");
+        size_t d = cfg.dim;
+        TRY(up16(w_embed, (size_t)cfg.vocab * d, embed));
+        if (w_head) TRY(up16(w_head, (size_t)cfg.vocab * d, head));
+        else head = embed;
+        TRY(up16(w_norm, d, norm));
+        size_t slots = (size_t)lim.pages * lim.page;
+        size_t kv_bytes = slots * cfg.kv_heads * cfg.head_dim * 2;
+        const u16* p = w_layers;
+        size_t hd = (size_t)cfg.heads * cfg.head_dim, qr = qkv_rows(cfg), ff = cfg.ffn;
+        for (int i = 0; i < cfg.layers; i++) {
+            Layer L;
+            TRY(up16(p, d, L.n1));
+            p += d;
+            TRY(up16(p, qr * d, L.wqkv));
+            p += qr * d;
+            TRY(up16(p, d * hd, L.wo));
+            p += d * hd;
+            TRY(up16(p, d, L.n2));
+            p += d;
+            TRY(up16(p, ff * d, L.wg));
+            p += ff * d;
+            TRY(up16(p, ff * d, L.wu));
+            p += ff * d;
+            TRY(up16(p, d * ff, L.wd));
+            p += d * ff;
+            TRY(alloc(kv_bytes, L.kc));
+            TRY(alloc(kv_bytes, L.vc));
+            layers.push_back(L);
+        }
+        std::vector<float> cs, sn;
+        rope_tables(cfg, cs, sn);
+        TRY(alloc(cs.size() * 4, cos));
+        TRY(write(cos, 0, cs.data(), cs.size() * 4));
+        TRY(alloc(sn.size() * 4, sin));
+        TRY(write(sin, 0, sn.data(), sn.size() * 4));
+        size_t t = padded(lim.max_tokens);
+        size_t gd = (size_t)cfg.kv_heads * cfg.head_dim;
+        TRY(alloc(t * d * 4, x));
+        TRY(alloc(t * d * 2, h));
+        TRY(alloc(t * qr * 2, qkv));
+        TRY(alloc(t * hd * 2, q));
+        TRY(alloc(t * gd * 2, k));
+        TRY(alloc(t * gd * 2, v));
+        TRY(alloc(t * hd * 2, o));
+        TRY(alloc(t * ff * 2, mlp));
+        TRY(alloc(t * d * 2, last));
+        TRY(alloc(t * (size_t)cfg.vocab * 4, logits));
+        TRY(alloc(t * 4, tok));
+        TRY(alloc(t * 4, pos));
+        TRY(alloc(t * 4, slot));
+        TRY(alloc(t * 4, idx));
+        TRY(alloc(t * (size_t)lim.max_seq_pages * 4, table));
+        TRY(alloc(t * 4, lens));
+        TRY(alloc(t * 4, starts));
+        return 0;
+    }
+
+    // Engine::launch_all (src/llm/engine.rs:359-529).
+    int launch_all(size_t t, bool prefill, size_t bw) {
+        int64_t dm = cfg.dim, nh = cfg.heads, ng = cfg.kv_heads, hd = cfg.head_dim;
+        int64_t w = qkv_rows(cfg), f = cfg.ffn, vv = cfg.vocab;
+        int64_t ns = (int64_t)lim.pages * lim.page, mp = lim.max_seq_pages, T = (int64_t)t;
+        int64_t bc = 1;
+        while (bc < dm) bc <<= 1;
+        float scale = 1.0f / std::sqrt((float)hd);
+        uint64_t scale_bits = 0, eps_bits = 0;
+        std::memcpy(&scale_bits, &scale, 4);
+        std::memcpy(&eps_bits, &cfg.eps, 4);
+        auto B = [](const Buf& b) { return Arg{Arg::BUF, b.p}; };
+        Arg SC{Arg::F32, scale_bits}, EPS{Arg::F32, eps_bits};
+        int embed_k, norm_k, qkv_k, rope_k, kvw_k, att_k, oproj_k, gu_k, down_k;
+        TRY(kernel("embed", {{T}, {vv, dm}, {T, dm}}, {{"BD", std::min<int64_t>(bc, 1024)}}, 4, &embed_k));
+        TRY(kernel("rmsnorm", {{T, dm}, {dm}, {T, dm}}, {{"BC", bc}}, 4, &norm_k));
+        const Layer& l0 = layers[0];
+        TRY(mm("linear", {{T, dm}, {w, dm}, {T, w}}, false, {B(h), B(l0.wqkv), B(qkv)}, &qkv_k));
+        int64_t npos = cfg.max_pos;
+        TRY(kernel("rope_q", {{T, w}, {T}, {npos, hd / 2}, {npos, hd / 2}, {T, nh, hd}}, {}, 1, &rope_k));
+        TRY(kernel("kv_write",
+                   {{T, w}, {T}, {T}, {npos, hd / 2}, {npos, hd / 2}, {ns, ng, hd}, {ns, ng, hd}, {T, ng, hd},
+                    {T, ng, hd}},
+                   {}, 1, &kvw_k));
+        if (prefill) {
+            TRY(kernel("prefill_attention", {{T, nh, hd}, {T, ng, hd}, {T, ng, hd}, {T}, {T, nh, hd}},
+                       {{"BM", 64}, {"BN", 64}}, 4, &att_k));
+        } else {
+            int64_t p = lim.page;
+            TRY(kernel("decode_attention",
+                       {{T, nh, hd}, {lim.pages, p, ng, hd}, {lim.pages, p, ng, hd}, {T, mp}, {T}, {T, nh, hd}}, {}, 1,
+                       &att_k));
+        }
+        TRY(mm("linear_residual", {{T, nh * hd}, {dm, nh * hd}, {T, dm}}, false, {B(o), B(l0.wo), B(x)}, &oproj_k));
+        TRY(mm("gate_up", {{T, dm}, {f, dm}, {f, dm}, {T, f}}, true, {B(h), B(l0.wg), B(l0.wu), B(mlp)}, &gu_k));
+        TRY(mm("linear_residual", {{T, f}, {dm, f}, {T, dm}}, false, {B(mlp), B(l0.wd), B(x)}, &down_k));
+
+        TRY(launch(embed_k, {B(tok), B(embed), B(x)}));
+        for (auto& L : layers) {
+            TRY(launch(norm_k, {B(x), B(L.n1), B(h), EPS}));
+            TRY(launch(qkv_k, {B(h), B(L.wqkv), B(qkv)}));
+            TRY(launch(rope_k, {B(qkv), B(pos), B(cos), B(sin), B(q)}));
+            TRY(launch(kvw_k, {B(qkv), B(pos), B(slot), B(cos), B(sin), B(L.kc), B(L.vc), B(k), B(v)}));
+            if (prefill) TRY(launch(att_k, {B(q), B(k), B(v), B(starts), B(o), SC}));
+            else TRY(launch(att_k, {B(q), B(L.kc), B(L.vc), B(table), B(lens), B(o), SC}));
+            TRY(launch(oproj_k, {B(o), B(L.wo), B(x)}));
+            TRY(launch(norm_k, {B(x), B(L.n2), B(h), EPS}));
+            TRY(launch(gu_k, {B(h), B(L.wg), B(L.wu), B(mlp)}));
+            TRY(launch(down_k, {B(mlp), B(L.wd), B(x)}));
+        }
+        if (bw == 0) return 0;
+        int fin_k, head_k;
+        int64_t BW = (int64_t)bw;
+        TRY(kernel("rmsnorm_rows", {{T, dm}, {BW}, {dm}, {BW, dm}}, {{"BC", bc}}, 4, &fin_k));
+        TRY(mm("logits", {{BW, dm}, {vv, dm}, {BW, vv}}, false, {B(last), B(head), B(logits)}, &head_k));
+        TRY(launch(fin_k, {B(x), B(idx), B(norm), B(last), EPS}));
+        TRY(launch(head_k, {B(last), B(head), B(logits)}));
+        return 0;
+    }
+
+    // Engine::step (src/llm/engine.rs:275-354).
+    int step(size_t n, const int32_t* tokens, const int32_t* ps_in, const int32_t* slots, int mode,
+             const int32_t* st_in, size_t nseq, const int32_t* tables, const int32_t* ln_in, size_t nwant,
+             const int32_t* want, float* out) {
+        if (n == 0 || n > (size_t)lim.max_tokens) {
+            std::ostringstream e;
+            e << "a step of " << n << " tokens (at most " << lim.max_tokens << ")";
+            return tsl_fail(TSL_ERR_ARG, e.str());
+        }
+        size_t t = padded(n);
+        int32_t ns = lim.pages * lim.page;
+        std::vector<int32_t> tk(tokens, tokens + n), ps(ps_in, ps_in + n), sl(slots, slots + n);
+        tk.resize(t, 0);
+        ps.resize(t, 0);
+        sl.resize(t, ns);  // padding rows write to no slot
+        TRY(write(tok, 0, tk.data(), t * 4));
+        TRY(write(pos, 0, ps.data(), t * 4));
+        TRY(write(slot, 0, sl.data(), t * 4));
+        size_t mp = lim.max_seq_pages;
+        if (mode == PREFILL || mode == PACKED) {
+            std::vector<int32_t> st(n, 0);
+            if (mode == PACKED) {
+                if (!st_in) return tsl_fail(TSL_ERR_ARG, "packed prefill: one start per token");
+                st.assign(st_in, st_in + n);
+            }
+            for (size_t i = n; i < t; i++) st.push_back((int32_t)i);  // padding rows start at themselves
+            TRY(write(starts, 0, st.data(), t * 4));
+        } else if (mode == DECODE) {
+            if (nseq > t) return tsl_fail(TSL_ERR_ARG, "decode: more sequences than rows");
+            std::vector<int32_t> tb(t * mp, 0), ln(t, 0);
+            for (size_t b = 0; b < nseq; b++) {
+                std::memcpy(&tb[b * mp], tables + b * mp, mp * 4);
+                ln[b] = ln_in[b];
+            }
+            TRY(write(table, 0, tb.data(), tb.size() * 4));
+            TRY(write(lens, 0, ln.data(), ln.size() * 4));
+        } else {
+            return tsl_fail(TSL_ERR_ARG, "unknown attention mode");
+        }
+        size_t bw = nwant ? padded(nwant) : 0;
+        if (bw) {
+            std::vector<int32_t> ix(want, want + nwant);
+            ix.resize(bw, 0);
+            TRY(write(idx, 0, ix.data(), bw * 4));
+        }
+        bool prefill = mode != DECODE;
+        if (!prefill && graphs && bw == t) {
+            auto it = graph.find(t);
+            if (it != graph.end()) {
+                TRY(tsl_replay(it->second));
+            } else {
+                TRY(launch_all(t, false, bw));
+                TRY(tsl_sync());
+                TRY(tsl_capture_begin());
+                int r = launch_all(t, false, bw);
+                int g = -1;
+                int r2 = tsl_capture_end(&g);
+                TRY(r);
+                TRY(r2);
+                graph[t] = g;
+            }
+        } else {
+            TRY(launch_all(t, prefill, bw));
+        }
+        if (nwant == 0) return 0;
+        return tsl_download(out, logits.p, nwant * (size_t)cfg.vocab * 4);
+    }
+};
+
+std::vector<std::unique_ptr<Engine>> g_engines;
+
+Engine* get(int e) {
+    if (e < 0 || e >= (int)g_engines.size() || !g_engines[e]) return nullptr;
+    return g_engines[e].get();
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsl_weights_sizes(const tsl_config* cfg, size_t* embed, size_t* per_layer, size_t* norm, size_t* head) {
+    *embed = (size_t)cfg->vocab * cfg->dim;
+    *per_layer = (size_t)layer_elems(*cfg);
+    *norm = cfg->dim;
+    *head = (size_t)cfg->vocab * cfg->dim;
+    return 0;
+}
+
+// Weights::random (src/llm/mod.rs:80-108).
+int tsl_weights_random(const tsl_config* cfg, uint64_t seed, uint16_t* embed, uint16_t* layers, uint16_t* norm,
+                       uint16_t* head) {
+    const tsl_config& c = *cfg;
+    Rng r(seed);
+    auto m = [&](int64_t rows, int64_t cols, u16* out) {
+        float sc = 1.0f / std::sqrt((float)cols);
+        for (int64_t i = 0; i < rows * cols; i++) out[i] = to_f16(r.uniform() * sc);
+    };
+    u16 one = to_f16(1.0f);
+    int64_t d = c.dim, hd = (int64_t)c.heads * c.head_dim, qr = qkv_rows(c);
+    u16* p = layers;
+    for (int l = 0; l < c.layers; l++) {
+        std::fill(p, p + d, one);
+        p += d;
+        m(qr, d, p);
+        p += qr * d;
+        m(d, hd, p);
+        p += d * hd;
+        std::fill(p, p + d, one);
+        p += d;
+        m(c.ffn, d, p);
+        p += (int64_t)c.ffn * d;
+        m(c.ffn, d, p);
+        p += (int64_t)c.ffn * d;
+        m(d, c.ffn, p);
+        p += d * c.ffn;
+    }
+    m(c.vocab, d, embed);
+    for (int64_t i = 0; i < (int64_t)c.vocab * d; i++) embed[i] = to_f16(from_f16(embed[i]) * 8.0f);
+    std::fill(norm, norm + d, one);
+    m(c.vocab, d, head);
+    return 0;
+}
+
+int tsl_engine_new(const tsl_config* cfg, const tsl_limits* lim, const uint16_t* embed, const uint16_t* layers,
+                   const uint16_t* norm, const uint16_t* head, int* engine) {
+    auto e = std::make_unique<Engine>();
+    TRY(e->init(*cfg, *lim, embed, layers, norm, head));
+    g_engines.push_back(std::move(e));
+    *engine = (int)g_engines.size() - 1;
+    return 0;
+}
+
+int tsl_engine_free(int engine) {
+    Engine* e = get(engine);
+    if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
+    tsl_sync();
+    Buf* bufs[] = {&e->embed, &e->norm, &e->cos, &e->sin, &e->x, &e->h, &e->qkv, &e->q, &e->k, &e->v,
+                   &e->o, &e->mlp, &e->last, &e->logits, &e->tok, &e->pos, &e->slot, &e->idx, &e->table,
+                   &e->lens, &e->starts};
+    if (e->head.p != e->embed.p) tsl_free(e->head.p);
+    for (Buf* b : bufs)
+        if (b->p) tsl_free(b->p);
+    for (auto& L : e->layers)
+        for (Buf* b : {&L.n1, &L.wqkv, &L.wo, &L.n2, &L.wg, &L.wu, &L.wd, &L.kc, &L.vc}) tsl_free(b->p);
+    g_engines[engine].reset();
+    return 0;
+}
+
+int tsl_engine_set(int engine, int graphs, int tune) {
+    Engine* e = get(engine);
+    if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
+    e->graphs = graphs != 0;
+    e->tune = tune != 0;
+    return 0;
+}
+
+int tsl_engine_step(int engine, int n, const int32_t* tokens, const int32_t* pos, const int32_t* slots, int mode,
+                    const int32_t* starts, int nseq, const int32_t* tables, const int32_t* lens, int nwant,
+                    const int32_t* want, float* logits) {
+    Engine* e = get(engine);
+    if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
+    if (n < 0 || nwant < 0 || nseq < 0) return tsl_fail(TSL_ERR_ARG, "negative count");
+    return e->step((size_t)n, tokens, pos, slots, mode, starts, (size_t)nseq, tables, lens, (size_t)nwant, want,
+                   logits);
+}
+
+// sched::generate_with (src/llm/sched.rs:52-179).
+int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* offsets, const int32_t* max_new,
+                 int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats) {
+    Engine* e = get(engine);
+    if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
+    using clk = std::chrono::steady_clock;
+    auto start = clk::now();
+    const int p = e->lim.page;
+    const int vocab = e->cfg.vocab;
+    const size_t mp = e->lim.max_seq_pages;
+    std::vector<int32_t> free_pages;
+    for (int i = e->lim.pages - 1; i >= 0; i--) free_pages.push_back(i);
+    std::deque<int> waiting;
+    for (int i = 0; i < nreq; i++) waiting.push_back(i);
+    struct Seq {
+        int id;
+        std::vector<int32_t> pages;
+        size_t len;
+        int32_t last;
+        int left;
+    };
+    std::vector<Seq> running;
+    std::vector<size_t> out_base(nreq, 0);
+    for (int i = 1; i < nreq; i++) out_base[i] = out_base[i - 1] + max_new[i - 1];
+    for (int i = 0; i < nreq; i++) out_counts[i] = 0;
+    tsl_stats st{};
+    max_batch = std::min(max_batch, e->lim.max_tokens);
+    const int eos = e->cfg.eos;
+    auto emit = [&](int id, int32_t t) { out_tokens[out_base[id] + out_counts[id]++] = t; };
+    while (!waiting.empty() || !running.empty()) {
+        std::vector<std::pair<int, std::vector<int32_t>>> admit;
+        size_t tokens = 0;
+        while (!waiting.empty()) {
+            int id = waiting.front();
+            size_t plen = (size_t)(offsets[id + 1] - offsets[id]);
+            size_t need = (plen + max_new[id] + p - 1) / p;
+            if (plen == 0 || plen > (size_t)e->lim.max_tokens || need > mp) {
+                std::ostringstream m;
+                m << "request " << id << ": prompt of " << plen << " tokens does not fit";
+                return tsl_fail(TSL_ERR_ARG, m.str());
+            }
+            bool room = (int)(running.size() + admit.size()) < max_batch && tokens + plen <= (size_t)e->lim.max_tokens;
+            if (!room || need > free_pages.size() || (!packed && !admit.empty())) break;
+            waiting.pop_front();
+            tokens += plen;
+            std::vector<int32_t> pages;
+            for (size_t i = 0; i < need; i++) {
+                pages.push_back(free_pages.back());
+                free_pages.pop_back();
+            }
+            admit.push_back({id, pages});
+        }
+        if (!admit.empty()) {
+            std::vector<int32_t> toks, pos, slots, starts, last;
+            for (auto& a : admit) {
+                const int32_t* pr = prompts + offsets[a.first];
+                size_t plen = (size_t)(offsets[a.first + 1] - offsets[a.first]);
+                int32_t s0 = (int32_t)toks.size();
+                for (size_t i = 0; i < plen; i++) {
+                    toks.push_back(pr[i]);
+                    pos.push_back((int32_t)i);
+                    slots.push_back(a.second[i / p] * p + (int32_t)(i % p));
+                    starts.push_back(s0);
+                }
+                last.push_back((int32_t)toks.size() - 1);
+            }
+            std::vector<float> logits(last.size() * (size_t)vocab);
+            int mode = admit.size() == 1 ? PREFILL : PACKED;
+            TRY(e->step(toks.size(), toks.data(), pos.data(), slots.data(), mode, starts.data(), 0, nullptr, nullptr,
+                        last.size(), last.data(), logits.data()));
+            st.prefill_steps++;
+            st.prompt_tokens += toks.size();
+            for (size_t i = 0; i < admit.size(); i++) {
+                int id = admit[i].first;
+                int32_t t = (int32_t)argmax(&logits[i * vocab], vocab);
+                emit(id, t);
+                size_t plen = (size_t)(offsets[id + 1] - offsets[id]);
+                Seq s{id, admit[i].second, plen, t, max_new[id] - 1};
+                if (s.left == 0 || t == eos) {
+                    free_pages.insert(free_pages.end(), s.pages.begin(), s.pages.end());
+                } else {
+                    running.push_back(s);
+                }
+            }
+            continue;
+        }
+        if (running.empty()) continue;
+        auto t0 = clk::now();
+        size_t nb = running.size();
+        std::vector<int32_t> toks, pos, slots, tables(nb * mp, 0), lens, want;
+        for (size_t b = 0; b < nb; b++) {
+            const Seq& s = running[b];
+            toks.push_back(s.last);
+            pos.push_back((int32_t)s.len);
+            slots.push_back(s.pages[s.len / p] * p + (int32_t)(s.len % p));
+            std::copy(s.pages.begin(), s.pages.end(), tables.begin() + b * mp);
+            lens.push_back((int32_t)s.len + 1);
+            want.push_back((int32_t)b);
+        }
+        std::vector<float> logits(nb * (size_t)vocab);
+        TRY(e->step(nb, toks.data(), pos.data(), slots.data(), DECODE, nullptr, nb, tables.data(), lens.data(), nb,
+                    want.data(), logits.data()));
+        st.decode_steps++;
+        st.largest_batch = std::max<int64_t>(st.largest_batch, nb);
+        st.decode_tokens += nb;
+        std::vector<Seq> keep;
+        for (size_t b = 0; b < nb; b++) {
+            Seq s = running[b];
+            int32_t t = (int32_t)argmax(&logits[b * vocab], vocab);
+            s.len++;
+            s.last = t;
+            s.left--;
+            emit(s.id, t);
+            if (s.left == 0 || t == eos) {
+                free_pages.insert(free_pages.end(), s.pages.begin(), s.pages.end());
+            } else {
+                keep.push_back(s);
+            }
+        }
+        running = keep;
+        st.decode_seconds += std::chrono::duration<double>(clk::now() - t0).count();
+    }
+    for (int i = 0; i < nreq; i++) st.generated += out_counts[i];
+    st.seconds = std::chrono::duration<double>(clk::now() - start).count();
+    if (stats) *stats = st;
+    return 0;
+}
+
+}  // extern "C"

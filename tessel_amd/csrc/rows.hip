@@ -1,0 +1,371 @@
+// HBM-bound row and elementwise kernels: basic.tl softmax (:10-17),
+// rmsnorm (:20-26) and add (:3-7); llm.tl embed (:10-16), rmsnorm (:19-25),
+// rmsnorm_rows (:175-182), rope_q (:78-88) and kv_write (:93-112).
+//
+// A row is owned by one 64-lane wavefront: it is read once with 16-byte
+// loads into registers, reduced across the wavefront (xor butterflies) and
+// written once, so each element crosses HBM once each way. Rows longer
+// than the register budget take a second, cache-resident pass.
+#include "common.h"
+
+namespace {
+
+constexpr int ROWS_PER_WG = 4;  // one wavefront per row, 4 per workgroup
+
+// ---------------------------------------------------------------- softmax
+// Y[r, c] = exp(x - max) / sum(exp(x - max)) over the first ncols = min(BC, C)
+// columns; columns past C read -inf (kernels/basic.tl:13), so they add 0.
+template <int NV>
+__global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ X, float* __restrict__ Y, int R, int C,
+                                                      int ncols) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * ROWS_PER_WG + (threadIdx.x >> 6);
+    if (row >= R) return;
+    const float* x = X + (size_t)row * C;
+    float* y = Y + (size_t)row * C;
+    const bool vec = (C % 4) == 0;
+    float v[NV][4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = i * 256 + lane * 4;
+        if (vec && c + 4 <= ncols) {
+            float4v t = *reinterpret_cast<const float4v*>(x + c);
+            for (int e = 0; e < 4; e++) v[i][e] = t[e];
+        } else {
+            for (int e = 0; e < 4; e++) v[i][e] = (c + e < ncols) ? x[c + e] : -INFINITY;
+        }
+        for (int e = 0; e < 4; e++) m = fmaxf(m, v[i][e]);
+    }
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+        for (int e = 0; e < 4; e++) {
+            v[i][e] = expf(v[i][e] - m);
+            s += v[i][e];
+        }
+    s = wave_sum(s);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = i * 256 + lane * 4;
+        if (vec && c + 4 <= ncols) {
+            float4v t;
+            for (int e = 0; e < 4; e++) t[e] = v[i][e] / s;
+            *reinterpret_cast<float4v*>(y + c) = t;
+        } else {
+            for (int e = 0; e < 4; e++)
+                if (c + e < ncols) y[c + e] = v[i][e] / s;
+        }
+    }
+}
+
+// Rows longer than the register tile: a max/sum pass, then the writes.
+__global__ __launch_bounds__(256) void softmax_long_kernel(const float* __restrict__ X, float* __restrict__ Y, int R,
+                                                           int C, int ncols) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * ROWS_PER_WG + (threadIdx.x >> 6);
+    if (row >= R) return;
+    const float* x = X + (size_t)row * C;
+    float* y = Y + (size_t)row * C;
+    float m = -INFINITY, s = 0.0f;
+    for (int c = lane; c < ncols; c += 64) {
+        float t = x[c];
+        float m2 = fmaxf(m, t);
+        s = s * expf(m - m2) + expf(t - m2);
+        m = m2;
+    }
+    float mw = wave_max(m);
+    s = wave_sum(m == -INFINITY ? 0.0f : s * expf(m - mw));
+    for (int c = lane; c < ncols; c += 64) y[c] = expf(x[c] - mw) / s;
+}
+
+// ---------------------------------------------------------------- rmsnorm
+// y = x * (1 / sqrt(sum(x^2 over BC columns) / n + eps)) * w, over the
+// first ncols = min(BC, C) columns (columns past C read 0). XT is f16
+// (basic.tl) or f32 (llm.tl); `rows` (rmsnorm_rows) gathers the input row.
+template <typename XT, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ X, const int* __restrict__ idx,
+                                                      int xrows, const u16* __restrict__ W, u16* __restrict__ Y,
+                                                      int R, int C, int ncols, float n, float eps) {
+    constexpr int E = 16 / sizeof(XT);  // elements per 16-byte load
+    const int lane = threadIdx.x & 63, row = blockIdx.x * ROWS_PER_WG + (threadIdx.x >> 6);
+    if (row >= R) return;
+    int src = row;
+    if (idx) src = idx[row];
+    const bool rin = src >= 0 && src < xrows;
+    const XT* x = X + (size_t)(rin ? src : 0) * C;
+    u16* y = Y + (size_t)row * C;
+    const bool vec = (C % E) == 0;
+    float v[NV][E];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = (i * 64 + lane) * E;
+        if (rin && vec && c + E <= ncols) {
+            if constexpr (sizeof(XT) == 2) {
+                u32x4 t = *reinterpret_cast<const u32x4*>(x + c);
+                for (int e = 0; e < E; e++) v[i][e] = h2f((u16)(t[e >> 1] >> (16 * (e & 1))));
+            } else {
+                float4v t = *reinterpret_cast<const float4v*>(x + c);
+                for (int e = 0; e < E; e++) v[i][e] = t[e];
+            }
+        } else {
+            for (int e = 0; e < E; e++) {
+                float t = 0.0f;
+                if (rin && c + e < ncols) {
+                    if constexpr (sizeof(XT) == 2) t = h2f(x[c + e]);
+                    else t = x[c + e];
+                }
+                v[i][e] = t;
+            }
+        }
+        for (int e = 0; e < E; e++) ss += v[i][e] * v[i][e];
+    }
+    ss = wave_sum(ss);
+    const float rs = 1.0f / sqrtf(ss / n + eps);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = (i * 64 + lane) * E;
+        if (vec && c + E <= ncols) {
+            // E outputs: 8 halves (16 bytes) for f16 input rows, 4 (8 bytes) for f32.
+            uint32_t o[E / 2];
+            for (int p = 0; p < E / 2; p++) {
+                u16 lo = f2h(v[i][2 * p] * rs * h2f(W[c + 2 * p]));
+                u16 hi = f2h(v[i][2 * p + 1] * rs * h2f(W[c + 2 * p + 1]));
+                o[p] = (uint32_t)lo | ((uint32_t)hi << 16);
+            }
+            if constexpr (E == 8) {
+                *reinterpret_cast<u32x4*>(y + c) = u32x4{o[0], o[1], o[2], o[3]};
+            } else {
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<u32x2*>(y + c) = u32x2{o[0], o[1]};
+            }
+        } else {
+            for (int e = 0; e < E; e++)
+                if (c + e < ncols) y[c + e] = f2h(v[i][e] * rs * h2f(W[c + e]));
+        }
+    }
+}
+
+template <typename XT>
+__global__ __launch_bounds__(256) void rmsnorm_long_kernel(const XT* __restrict__ X, const int* __restrict__ idx,
+                                                           int xrows, const u16* __restrict__ W, u16* __restrict__ Y,
+                                                           int R, int C, int ncols, float n, float eps) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * ROWS_PER_WG + (threadIdx.x >> 6);
+    if (row >= R) return;
+    int src = idx ? idx[row] : row;
+    const bool rin = src >= 0 && src < xrows;
+    const XT* x = X + (size_t)(rin ? src : 0) * C;
+    auto ld = [&](int c) -> float {
+        if (!rin) return 0.0f;
+        if constexpr (sizeof(XT) == 2) return h2f(x[c]);
+        else return x[c];
+    };
+    float ss = 0.0f;
+    for (int c = lane; c < ncols; c += 64) {
+        float t = ld(c);
+        ss += t * t;
+    }
+    const float rs = 1.0f / sqrtf(wave_sum(ss) / n + eps);
+    for (int c = lane; c < ncols; c += 64) Y[(size_t)row * C + c] = f2h(ld(c) * rs * h2f(W[c]));
+}
+
+template <typename XT>
+int run_rmsnorm(const XT* X, const int* idx, int xrows, const u16* W, u16* Y, int R, int C, int ncols, float eps,
+                hipStream_t s, const char* what) {
+    if (R == 0) return 0;
+    dim3 grid((R + ROWS_PER_WG - 1) / ROWS_PER_WG);
+    constexpr int E = 16 / sizeof(XT);
+    const float n = (float)C;
+    if (ncols <= 64 * E * 4)
+        hipLaunchKernelGGL((rmsnorm_kernel<XT, 4>), grid, dim3(256), 0, s, X, idx, xrows, W, Y, R, C, ncols, n, eps);
+    else if (ncols <= 64 * E * 8)
+        hipLaunchKernelGGL((rmsnorm_kernel<XT, 8>), grid, dim3(256), 0, s, X, idx, xrows, W, Y, R, C, ncols, n, eps);
+    else
+        hipLaunchKernelGGL((rmsnorm_long_kernel<XT>), grid, dim3(256), 0, s, X, idx, xrows, W, Y, R, C, ncols, n, eps);
+    return TSL_LAUNCHED(what);
+}
+
+// ---------------------------------------------------------------- add, embed
+
+__global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ X, const float* __restrict__ Y,
+                                                  float* __restrict__ Z, long n) {
+    long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i + 4 <= n) {
+        float4v a = *reinterpret_cast<const float4v*>(X + i), b = *reinterpret_cast<const float4v*>(Y + i);
+        *reinterpret_cast<float4v*>(Z + i) = a + b;
+    } else {
+        for (; i < n; i++) Z[i] = X[i] + Y[i];
+    }
+}
+
+// X[t, :] = f32(E[tok[t], :]); a token outside [0, V) reads zeros.
+__global__ __launch_bounds__(256) void embed_kernel(const int* __restrict__ tok, const u16* __restrict__ E,
+                                                    float* __restrict__ X, int T, int V, int Dm) {
+    const int t = blockIdx.y;
+    const int row = tok[t];
+    const bool in = row >= 0 && row < V;
+    for (int c = (blockIdx.x * 256 + threadIdx.x) * 8; c < Dm; c += gridDim.x * 256 * 8) {
+        float* x = X + (size_t)t * Dm + c;
+        if (c + 8 <= Dm && (Dm % 8) == 0) {
+            float4v a, b;
+            if (in) {
+                u32x4 h = *reinterpret_cast<const u32x4*>(E + (size_t)row * Dm + c);
+                for (int e = 0; e < 4; e++) a[e] = h2f((u16)(h[e >> 1] >> (16 * (e & 1))));
+                for (int e = 0; e < 4; e++) b[e] = h2f((u16)(h[2 + (e >> 1)] >> (16 * (e & 1))));
+            } else {
+                a = float4v{0, 0, 0, 0};
+                b = a;
+            }
+            *reinterpret_cast<float4v*>(x) = a;
+            *reinterpret_cast<float4v*>(x + 4) = b;
+        } else {
+            for (int e = 0; e < 8 && c + e < Dm; e++) x[e] = in ? h2f(E[(size_t)row * Dm + c + e]) : 0.0f;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- rotary
+// rope_q: Q[t, h, i] = x1 c - x2 s and Q[t, h, D2 + i] = x2 c + x1 s with
+// x1 = QKV[t, h D + i], x2 = QKV[t, h D + D2 + i], (c, s) at pos[t].
+__global__ __launch_bounds__(256) void rope_q_kernel(const u16* __restrict__ QKV, const int* __restrict__ pos,
+                                                     const float* __restrict__ Cs, const float* __restrict__ Sn,
+                                                     u16* __restrict__ Q, int T, int W, int NPOS, int D2, int H,
+                                                     int D) {
+    const long n = (long)T * H * D2;
+    for (long e = (long)blockIdx.x * 256 + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
+        const int i = e % D2, h = (e / D2) % H, t = e / ((long)D2 * H);
+        const int p = pos[t];
+        const bool pin = p >= 0 && p < NPOS;
+        const float c = pin ? Cs[(size_t)p * D2 + i] : 0.0f, s = pin ? Sn[(size_t)p * D2 + i] : 0.0f;
+        const int c1 = h * D + i, c2 = h * D + D2 + i;
+        const float x1 = c1 < W ? h2f(QKV[(size_t)t * W + c1]) : 0.0f;
+        const float x2 = c2 < W ? h2f(QKV[(size_t)t * W + c2]) : 0.0f;
+        u16* q = Q + ((size_t)t * H + h) * D;
+        if (i < D) q[i] = f2h(x1 * c - x2 * s);
+        if (D2 + i < D) q[D2 + i] = f2h(x2 * c + x1 * s);
+    }
+}
+
+// kv_write: the rotated keys and the values of kv head g into the paged
+// cache at slot[t] (dropped when outside [0, NS)) and into K, V [T, G, D].
+__global__ __launch_bounds__(256) void kv_write_kernel(const u16* __restrict__ QKV, const int* __restrict__ pos,
+                                                       const int* __restrict__ slot, const float* __restrict__ Cs,
+                                                       const float* __restrict__ Sn, u16* __restrict__ Kc,
+                                                       u16* __restrict__ Vc, u16* __restrict__ K, u16* __restrict__ V,
+                                                       int T, int W, int NPOS, int D2, int NS, int G, int D) {
+    const int nd = D2 > D ? D2 : D;
+    const long n = (long)T * G * nd;
+    for (long e = (long)blockIdx.x * 256 + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
+        const int i = e % nd, g = (e / nd) % G, t = e / ((long)nd * G);
+        const int p = pos[t], at = slot[t];
+        const bool pin = p >= 0 && p < NPOS, ain = at >= 0 && at < NS;
+        const long k0 = (long)W - 2L * G * D + (long)g * D;
+        u16* kc = Kc + ((size_t)(ain ? at : 0) * G + g) * D;
+        u16* vc = Vc + ((size_t)(ain ? at : 0) * G + g) * D;
+        u16* kk = K + ((size_t)t * G + g) * D;
+        u16* vv = V + ((size_t)t * G + g) * D;
+        if (i < D2) {
+            const float c = pin ? Cs[(size_t)p * D2 + i] : 0.0f, s = pin ? Sn[(size_t)p * D2 + i] : 0.0f;
+            const long c1 = k0 + i, c2 = k0 + D2 + i;
+            const float x1 = (c1 >= 0 && c1 < W) ? h2f(QKV[(size_t)t * W + c1]) : 0.0f;
+            const float x2 = (c2 >= 0 && c2 < W) ? h2f(QKV[(size_t)t * W + c2]) : 0.0f;
+            const u16 y1 = f2h(x1 * c - x2 * s), y2 = f2h(x2 * c + x1 * s);
+            if (i < D) {
+                if (ain) kc[i] = y1;
+                kk[i] = y1;
+            }
+            if (D2 + i < D) {
+                if (ain) kc[D2 + i] = y2;
+                kk[D2 + i] = y2;
+            }
+        }
+        if (i < D) {
+            const long cv = k0 + (long)G * D + i;
+            const u16 v = (cv >= 0 && cv < W) ? QKV[(size_t)t * W + cv] : (u16)0;
+            if (ain) vc[i] = v;
+            vv[i] = v;
+        }
+    }
+}
+
+int grid1(long n) {
+    long g = (n + 255) / 256;
+    return (int)(g < 1 ? 1 : (g > 65535 * 4 ? 65535 * 4 : g));
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- launchers
+
+int launch_softmax(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    int R = k.dim("R"), C = k.dim("C");
+    int ncols = (int)std::min<int64_t>(k.metav("BC"), C);
+    if (R == 0) return 0;
+    dim3 grid((R + ROWS_PER_WG - 1) / ROWS_PER_WG);
+    const float* X = P<float>(a[0]);
+    float* Y = P<float>(a[1]);
+    if (ncols <= 1024)
+        hipLaunchKernelGGL((softmax_kernel<4>), grid, dim3(256), 0, s, X, Y, R, C, ncols);
+    else if (ncols <= 4096)
+        hipLaunchKernelGGL((softmax_kernel<16>), grid, dim3(256), 0, s, X, Y, R, C, ncols);
+    else
+        hipLaunchKernelGGL(softmax_long_kernel, grid, dim3(256), 0, s, X, Y, R, C, ncols);
+    return TSL_LAUNCHED("softmax");
+}
+
+int launch_rmsnorm_basic(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    int R = k.dim("R"), C = k.dim("C");
+    int ncols = (int)std::min<int64_t>(k.metav("BC"), C);
+    return run_rmsnorm<u16>(P<u16>(a[0]), nullptr, R, P<u16>(a[1]), P<u16>(a[2]), R, C, ncols, arg_f32(a[3]), s,
+                            "rmsnorm");
+}
+
+int launch_add(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    long N = k.dim("N");
+    if (N == 0) return 0;
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((N + 1023) / 1024)), dim3(256), 0, s, P<float>(a[0]),
+                       P<float>(a[1]), P<float>(a[2]), N);
+    return TSL_LAUNCHED("add");
+}
+
+int launch_embed(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    int T = k.dim("T"), V = k.dim("V"), Dm = k.dim("Dm");
+    if (T == 0) return 0;
+    dim3 grid((Dm + 2047) / 2048, T);
+    hipLaunchKernelGGL(embed_kernel, grid, dim3(256), 0, s, P<int>(a[0]), P<u16>(a[1]), P<float>(a[2]), T, V, Dm);
+    return TSL_LAUNCHED("embed");
+}
+
+int launch_llm_rmsnorm(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    int T = k.dim("T"), Dm = k.dim("Dm");
+    int ncols = (int)std::min<int64_t>(k.metav("BC"), Dm);
+    return run_rmsnorm<float>(P<float>(a[0]), nullptr, T, P<u16>(a[1]), P<u16>(a[2]), T, Dm, ncols, arg_f32(a[3]), s,
+                              "rmsnorm");
+}
+
+int launch_rmsnorm_rows(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    int T = k.dim("T"), B = k.dim("B"), Dm = k.dim("Dm");
+    int ncols = (int)std::min<int64_t>(k.metav("BC"), Dm);
+    return run_rmsnorm<float>(P<float>(a[0]), P<int>(a[1]), T, P<u16>(a[2]), P<u16>(a[3]), B, Dm, ncols,
+                              arg_f32(a[4]), s, "rmsnorm_rows");
+}
+
+int launch_rope_q(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    int T = k.dim("T"), W = k.dim("W"), NPOS = k.dim("NPOS"), D2 = k.dim("D2"), H = k.dim("H"), D = k.dim("D");
+    long n = (long)T * H * D2;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(rope_q_kernel, dim3(grid1(n)), dim3(256), 0, s, P<u16>(a[0]), P<int>(a[1]), P<float>(a[2]),
+                       P<float>(a[3]), P<u16>(a[4]), T, W, NPOS, D2, H, D);
+    return TSL_LAUNCHED("rope_q");
+}
+
+int launch_kv_write(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    int T = k.dim("T"), W = k.dim("W"), NPOS = k.dim("NPOS"), D2 = k.dim("D2"), NS = k.dim("NS"), G = k.dim("G"),
+        D = k.dim("D");
+    long n = (long)T * G * std::max(D2, D);
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(kv_write_kernel, dim3(grid1(n)), dim3(256), 0, s, P<u16>(a[0]), P<int>(a[1]), P<int>(a[2]),
+                       P<float>(a[3]), P<float>(a[4]), P<u16>(a[5]), P<u16>(a[6]), P<u16>(a[7]), P<u16>(a[8]), T, W,
+                       NPOS, D2, NS, G, D);
+    return TSL_LAUNCHED("kv_write");
+}

@@ -1,0 +1,79 @@
+"""The engine (every step a sequence of the HIP llm.tl kernels) against the
+f32 reference model, on a small random Llama: tests/llm.rs:25-83 and
+:189-227 restated, plus graph replay against eager launches."""
+
+import numpy as np
+import pytest
+
+import oracle
+import tessel_amd as T
+
+pytestmark = pytest.mark.gpu
+
+
+def limits(page=8, pages=32, max_tokens=16, max_seq_pages=8):
+    return T.Limits(page, pages, max_tokens, max_seq_pages)
+
+
+def rel(got, want):
+    return np.abs(got - want).max() / np.abs(want).max()
+
+
+def test_prefill_and_batched_decode_match_the_reference(gpu):
+    cfg = T.Config.tiny()
+    w = T.weights_random(cfg, 7)
+    e = T.Engine(cfg, limits(), w)
+    prompt = [1, 17, 200, 33, 5, 99, 64, 3, 250, 12]
+    n = len(prompt)
+    got = e.step(prompt, list(range(n)), list(range(n)), T.Engine.PREFILL, want=[n - 1])
+    ocfg = oracle.Config.tiny()
+    want = oracle.forward(ocfg, w, prompt)
+    err = rel(got[0], want[n - 1])
+    print(f"prefill: logits within {err:.2e} of the reference", flush=True)
+    assert err < 2e-2
+    reqs = [([1, 5, 9], 6), (prompt, 4), ([1, 100, 101, 102, 103, 104, 105], 9)]
+    outs, st = e.generate(reqs, 3)
+    assert st.largest_batch == 3
+    exact = 0
+    for (p, m), toks in zip(reqs, outs):
+        assert len(toks) == m
+        seq = list(p)
+        for t in toks:
+            l = oracle.forward(ocfg, w, seq)[-1]
+            best = oracle.argmax(l)
+            scale = np.abs(l).max()
+            assert t == best or l[best] - l[t] < 2e-2 * scale, (t, best)
+            exact += t == best
+            seq.append(t)
+    print(f"generation: {exact} of {st.generated} tokens the reference's own choice", flush=True)
+    e.close()
+
+
+def test_packed_prefill_matches_one_prompt_per_step(gpu):
+    cfg = T.Config.tiny()
+    w = T.weights_random(cfg, 11)
+    lim = limits(page=8, pages=64, max_tokens=128, max_seq_pages=16)
+    long = [1 + (i * 37 % 250) for i in range(70)]
+    short = [1, 9, 42, 7, 200, 13, 5, 77, 31, 64, 2, 150, 99, 3, 18, 240, 6, 11, 120, 45]
+    reqs = [(long, 4), (short, 4)]
+    e = T.Engine(cfg, lim, w)
+    packed, st = e.generate(reqs, 2, packed=True)
+    assert st.prefill_steps == 1
+    e.close()
+    e = T.Engine(cfg, lim, w)
+    single, st = e.generate(reqs, 2, packed=False)
+    assert st.prefill_steps == 2
+    e.close()
+    assert packed == single
+
+
+def test_graph_replay_matches_eager(gpu):
+    cfg = T.Config.tiny()
+    w = T.weights_random(cfg, 5)
+    reqs = [([1, 2, 3, 4, 5], 12), ([9, 8, 7], 10), ([100 + i for i in range(12)], 8)]
+    outs = []
+    for graphs in (False, True):
+        e = T.Engine(cfg, limits(pages=64), w, graphs=graphs)
+        outs.append(e.generate(reqs, 3)[0])
+        e.close()
+    assert outs[0] == outs[1]

@@ -1,0 +1,350 @@
+"""The HIP kernels, launched through the C ABI, against the CPU oracle on
+identical seeded inputs: the reference's own test shapes (tests/interp.rs,
+tests/emu.rs, tests/llm.rs:108-187) and the BASELINE configs. Tolerance for
+float outputs (written in refs.parity): relative Frobenius error <= 1e-3
+and max |diff| <= 2e-2; integer, index and copy results bit-exact."""
+
+import numpy as np
+import pytest
+
+import oracle
+import tessel_amd as T
+from tests.refs import assert_close, attention_ref, matmul_ref, paged_ref, parity
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _open(gpu):
+    yield
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+# ---------------------------------------------------------------- matmul.tl
+
+@pytest.mark.parametrize("m,k,n", [(512, 512, 512), (100, 70, 90), (256, 256, 256), (1, 16, 8), (130, 264, 200)])
+def test_matmul_vs_oracle(m, k, n):
+    _say("matmul", m, k, n)
+    r = oracle.Rng(7 + m)
+    a, b = r.tensor("f16", [m, k]), r.tensor("f16", [k, n])
+    want = oracle.matmul(a, b, 128, 128, 32, 8, threads=8)
+    got = T.run("matmul", "matmul", [a, b, np.zeros((m, n), np.float16)], outputs=[2])[2]
+    parity("matmul", got, want)
+    assert_close("matmul vs f64", got, matmul_ref(a, b), 2e-3)
+
+
+def test_matmul_exact_integers():
+    _say("matmul integers")
+    rng = np.random.default_rng(4)
+    m, k, n = 300, 136, 264
+    a = rng.integers(-4, 5, (m, k)).astype(np.float16)
+    b = rng.integers(-4, 5, (k, n)).astype(np.float16)
+    want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float16)
+    got = T.run("matmul", "matmul", [a, b, np.zeros((m, n), np.float16)], outputs=[2])[2]
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("n", [1024, 2048, 4096])
+def test_matmul_large_sampled(n):
+    # A, B ~ N(0,1)/sqrt(K); checked at 512 sampled entries
+    # against f64 (as src/bench.rs:86-98 does) and, on a block of rows, against the oracle.
+    _say("matmul large", n)
+    rng = np.random.default_rng(n)
+    a = (rng.standard_normal((n, n)) / np.sqrt(n)).astype(np.float16)
+    b = (rng.standard_normal((n, n)) / np.sqrt(n)).astype(np.float16)
+    got = T.run("matmul", "matmul", [a, b, np.zeros((n, n), np.float16)], outputs=[2])[2]
+    i = rng.integers(0, n, 512)
+    j = rng.integers(0, n, 512)
+    want = np.einsum("sk,ks->s", a[i].astype(np.float64), b[:, j].astype(np.float64))
+    assert np.abs(got[i, j].astype(np.float64) - want).max() <= 2e-3 * max(1.0, np.abs(want).max())
+    rows = slice(n // 2, n // 2 + 128)
+    want_rows = oracle.matmul(np.ascontiguousarray(a[rows]), b, 128, 128, 32, 8, threads=8)
+    parity("matmul rows", got[rows], want_rows)
+
+
+def test_matmul_f32_and_linear_bias():
+    _say("matmul_f32, linear")
+    r = oracle.Rng(12)
+    m, k, n = 100, 70, 90
+    a, b = r.tensor("f32", [m, k]), r.tensor("f32", [k, n])
+    got = T.run("matmul", "matmul_f32", [a, b, np.zeros((m, n), np.float32)], outputs=[2])[2]
+    assert_close("matmul_f32", got, oracle.matmul_f32(a, b), 1e-5)
+    x, w, bias = r.tensor("f16", [m, k]), r.tensor("f16", [n, k]), r.tensor("f16", [n])
+    got = T.run("matmul", "linear", [x, w, bias, np.zeros((m, n), np.float16)], outputs=[3])[3]
+    parity("linear bias", got, oracle.linear_bias(x, w, bias))
+
+
+# ---------------------------------------------------------------- llm.tl matmuls
+
+MM_CASES = ["linear", "linear_residual", "logits", "gate_up"]
+
+
+def _mm_args(r, name, m, k, n, wscale=0.1):
+    x = r.tensor("f16", [m, k], 1.0)
+    w = r.tensor("f16", [n, k], wscale)
+    if name == "linear":
+        return [x, w, np.zeros((m, n), np.float16)], oracle.llm_linear(x, w)
+    if name == "linear_residual":
+        res = r.tensor("f32", [m, n], 1.0)
+        return [x, w, res], oracle.linear_residual(x, w, res)
+    if name == "logits":
+        return [x, w, np.zeros((m, n), np.float32)], oracle.logits(x, w)
+    w2 = r.tensor("f16", [n, k], wscale)
+    return [x, w, w2, np.zeros((m, n), np.float16)], oracle.gate_up(x, w, w2)
+
+
+@pytest.mark.parametrize("m", [16, 32, 64])
+@pytest.mark.parametrize("name", MM_CASES)
+def test_every_tuning_candidate(name, m):
+    # tests/llm.rs:108-187: each tile configuration the tuner may pick,
+    # within 1e-2 of the largest output.
+    _say("mm candidates", name, m)
+    r = oracle.Rng(5)
+    k, n = 256, 96
+    args, want = _mm_args(r, name, m, k, n)
+    for meta, warps in T.mm_candidates(m, name == "gate_up"):
+        got = T.run("llm", name, [a.copy() for a in args], meta=meta, warps=warps, outputs=[len(args) - 1])
+        got = got[len(args) - 1]
+        scale = np.abs(want).max()
+        err = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
+        assert err <= 1e-2 * scale, (name, m, meta, warps, err, scale)
+        parity(f"{name} m={m} {meta}", got, want)
+
+
+@pytest.mark.parametrize("m", [1, 16, 32, 128, 512])
+@pytest.mark.parametrize("name", MM_CASES)
+def test_llm_matmuls_tinyllama_shapes(name, m):
+    _say("llm mm", name, m)
+    r = oracle.Rng(100 + m)
+    k, n = {"linear": (2048, 2560), "linear_residual": (5632, 2048), "logits": (2048, 4000),
+            "gate_up": (2048, 5632)}[name]
+    args, want = _mm_args(r, name, m, k, n, wscale=1.0 / np.sqrt(k))
+    got = T.run("llm", name, args, outputs=[len(args) - 1])[len(args) - 1]
+    parity(f"{name} m={m}", got, want)
+
+
+# ---------------------------------------------------------------- attention
+
+@pytest.mark.parametrize("h,s,d", [(2, 150, 32), (2, 100, 32), (1, 40, 16), (4, 300, 64), (2, 200, 128)])
+def test_flash_attention_vs_oracle(h, s, d):
+    _say("flash", h, s, d)
+    r = oracle.Rng(4 + s)
+    q, k, v = (r.tensor("f16", [h, s, d]) for _ in range(3))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    want = oracle.flash_attention(q, k, v, scale, threads=8)
+    got = T.run("attention", "flash_attention", [q, k, v, np.zeros_like(q)], [T.F32(scale)], outputs=[3])[3]
+    parity("flash", got, want)
+    assert_close("flash vs f64", got, attention_ref(q, k, v, scale), 5e-3)
+
+
+@pytest.mark.parametrize("s", [512, 1024])
+def test_flash_attention_baseline_shapes(s):
+    # BASELINE config 3 (H 32, D 64) against the oracle.
+    _say("flash baseline", s)
+    rng = np.random.default_rng(s)
+    q, k, v = (rng.standard_normal((32, s, 64)).astype(np.float16) for _ in range(3))
+    want = oracle.flash_attention(q, k, v, 0.125, threads=8)
+    got = T.run("attention", "flash_attention", [q, k, v, np.zeros_like(q)], [T.F32(0.125)], outputs=[3])[3]
+    parity("flash baseline", got, want)
+
+
+@pytest.mark.parametrize("s", [2048, 4096])
+def test_flash_attention_long_sampled(s):
+    # Long sequences: sampled query rows against the f64 closed form
+    # (src/bench.rs:135-160 checks 4 rows); 16 rows of varied heads here.
+    _say("flash long", s)
+    rng = np.random.default_rng(s)
+    q, k, v = (rng.standard_normal((32, s, 64)).astype(np.float16) for _ in range(3))
+    got = T.run("attention", "flash_attention", [q, k, v, np.zeros_like(q)], [T.F32(0.125)], outputs=[3])[3]
+    for _ in range(16):
+        hh, i = int(rng.integers(0, 32)), int(rng.integers(0, s))
+        sc = k[hh, :i + 1].astype(np.float64) @ q[hh, i].astype(np.float64) * 0.125
+        e = np.exp(sc - sc.max())
+        want = e @ v[hh, :i + 1].astype(np.float64) / e.sum()
+        parity(f"flash row {hh},{i}", got[hh, i], want)
+
+
+def _packed(seed, lens, h, g, d):
+    r = oracle.Rng(seed)
+    s = sum(lens)
+    q = r.tensor("f16", [s, h, d])
+    k = r.tensor("f16", [s, g, d])
+    v = r.tensor("f16", [s, g, d])
+    starts = np.concatenate([np.full(l, sum(lens[:i]), np.int32) for i, l in enumerate(lens)])
+    return q, k, v, starts
+
+
+@pytest.mark.parametrize("lens,h,g,d", [([90], 4, 2, 16), ([70, 20], 4, 2, 16), ([512, 512], 32, 4, 64),
+                                         ([300, 5, 130, 64], 8, 2, 64), ([1000], 32, 4, 64)])
+def test_prefill_attention_vs_oracle(lens, h, g, d):
+    _say("prefill", lens, h, g, d)
+    q, k, v, starts = _packed(11 + len(lens), lens, h, g, d)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    want = oracle.prefill_attention(q, k, v, starts, scale, threads=8)
+    got = T.run("llm", "prefill_attention", [q, k, v, starts, np.zeros_like(q)], [T.F32(scale)], outputs=[4])[4]
+    parity("prefill", got, want)
+
+
+def test_paged_attention_reference_case():
+    # tests/interp.rs:126-136 and tests/emu.rs:174-175.
+    _say("paged")
+    r = oracle.Rng(5)
+    q, kc, vc, table, lens, scale = oracle.paged_case(r, 3, 2, 32, 16, [37, 1, 64])
+    want = oracle.decode_attention(q, kc, vc, table, lens, scale)
+    got = T.run("attention", "paged_attention", [q, kc, vc, table, lens, np.zeros_like(q)], [T.F32(scale)],
+                outputs=[5])[5]
+    parity("paged", got, want)
+    assert_close("paged vs f64", got, paged_ref(q, kc, vc, table, lens, scale), 3e-3)
+
+
+def decode_case(seed, b=64, h=32, g=8, d=128, p=16, lo=128, hi=4096, mp=None):
+    """lens ~ U[lo, hi], pages assigned by a seeded
+    permutation into int32 block tables, KV pool N(0,1) f16."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lo, hi + 1, b).astype(np.int32)
+    need = (lens + p - 1) // p
+    mp = int(need.max()) if mp is None else mp
+    npages = int(need.sum())
+    perm = rng.permutation(npages).astype(np.int32)
+    table = np.zeros((b, mp), np.int32)
+    o = 0
+    for i in range(b):
+        table[i, :need[i]] = perm[o:o + need[i]]
+        o += need[i]
+    q = rng.standard_normal((b, h, d)).astype(np.float16)
+    kc = rng.standard_normal((npages, p, g, d)).astype(np.float16)
+    vc = rng.standard_normal((npages, p, g, d)).astype(np.float16)
+    return q, kc, vc, table, lens, float(np.float32(1.0) / np.sqrt(np.float32(d)))
+
+
+def _decode(q, kc, vc, table, lens, scale):
+    return T.run("llm", "decode_attention", [q, kc, vc, table, lens, np.zeros_like(q)], [T.F32(scale)],
+                 outputs=[5])[5]
+
+
+@pytest.mark.parametrize("cfg", [dict(b=64, h=32, g=8, d=128, p=16),
+                                 dict(b=8, h=32, g=4, d=64, p=16, lo=1, hi=700),
+                                 dict(b=5, h=4, g=2, d=16, p=8, lo=0, hi=60),
+                                 dict(b=3, h=8, g=8, d=32, p=16, lo=1, hi=300)])
+def test_decode_attention_vs_oracle(cfg):
+    _say("decode", cfg)
+    q, kc, vc, table, lens, scale = decode_case(1, **cfg)
+    want = oracle.decode_attention(q, kc, vc, table, lens, scale, threads=8)
+    got = _decode(q, kc, vc, table, lens, scale)
+    parity("decode", got, want)
+
+
+def test_decode_attention_indexing_properties():
+    _say("decode properties")
+    q, kc, vc, table, lens, scale = decode_case(2, b=16, h=32, g=8, d=128, p=16, lo=1, hi=1000)
+    base = _decode(q, kc, vc, table, lens, scale)
+    # The same tokens at other pool positions: bit-identical (only the token order matters).
+    perm = np.random.default_rng(3).permutation(kc.shape[0])
+    inv = np.argsort(perm).astype(np.int32)
+    got = _decode(q, np.ascontiguousarray(kc[perm]), np.ascontiguousarray(vc[perm]), inv[table], lens, scale)
+    np.testing.assert_array_equal(got.view(np.uint16), base.view(np.uint16))
+    # Pages outside the pool read as zeros (scores 0, values 0), as the oracle says.
+    t2 = table.copy()
+    t2[3, 0] = kc.shape[0] + 5
+    t2[5, 1] = -7
+    want = oracle.decode_attention(q, kc, vc, t2, lens, scale, threads=8)
+    parity("decode oob pages", _decode(q, kc, vc, t2, lens, scale), want)
+    # lens 0 gives NaN rows; the rest unchanged.
+    l0 = lens.copy()
+    l0[[2, 9]] = 0
+    got = _decode(q, kc, vc, table, l0, scale)
+    assert np.isnan(got[[2, 9]].astype(np.float32)).all()
+    keep = [i for i in range(16) if i not in (2, 9)]
+    np.testing.assert_array_equal(got[keep].view(np.uint16), base[keep].view(np.uint16))
+    # Tokens past the table's MP * P read page 0 (the interpreter's out-of-range load).
+    tb = np.ascontiguousarray(table[:, :8])
+    l3 = np.minimum(lens, 8 * 16 + 40).astype(np.int32)
+    want = oracle.decode_attention(q, kc, vc, tb, l3, scale, threads=8)
+    parity("decode past table", _decode(q, kc, vc, tb, l3, scale), want)
+
+
+# ---------------------------------------------------------------- rows
+
+@pytest.mark.parametrize("rows,cols,bc", [(10, 700, 1024), (4096, 4096, 4096), (7, 5000, 8192), (3, 40, 16)])
+def test_softmax(rows, cols, bc):
+    _say("softmax", rows, cols, bc)
+    r = oracle.Rng(2)
+    x = r.tensor("f32", [rows, cols], 4.0)
+    want = oracle.softmax(x, BC=bc, threads=8)
+    got = T.run("basic", "softmax", [x, np.zeros_like(x)], meta=[("BC", bc)], outputs=[1])[1]
+    parity("softmax", got, want)
+    assert np.abs(got - want).max() <= 1e-6
+
+
+@pytest.mark.parametrize("rows,cols,bc", [(10, 700, 1024), (4096, 4096, 4096), (5, 9000, 16384), (4, 100, 64)])
+def test_rmsnorm_basic(rows, cols, bc):
+    _say("rmsnorm basic", rows, cols, bc)
+    r = oracle.Rng(3)
+    x = r.tensor("f16", [rows, cols], 2.0)
+    w = r.tensor("f16", [cols], 1.0)
+    want = oracle.rmsnorm_basic(x, w, 1e-5, BC=bc, threads=8)
+    got = T.run("basic", "rmsnorm", [x, w, np.zeros_like(x)], [T.F32(1e-5)], meta=[("BC", bc)], outputs=[2])[2]
+    parity("rmsnorm", got, want)
+
+
+def test_add_exact():
+    r = oracle.Rng(1)
+    for n in (3000, 1 << 20, 5):
+        x, y = r.tensor("f32", [n]), r.tensor("f32", [n])
+        got = T.run("basic", "add", [x, y, np.zeros_like(x)], outputs=[2])[2]
+        np.testing.assert_array_equal(got, x + y)
+
+
+@pytest.mark.parametrize("t,dm", [(16, 2048), (5, 64), (32, 2048), (3, 1000)])
+def test_llm_rows(t, dm):
+    _say("llm rows", t, dm)
+    r = oracle.Rng(8)
+    bc = 1 << (dm - 1).bit_length()
+    x = r.tensor("f32", [t, dm], 3.0)
+    w = r.tensor("f16", [dm], 1.0)
+    got = T.run("llm", "rmsnorm", [x, w, np.zeros((t, dm), np.float16)], [T.F32(1e-5)], meta=[("BC", bc)],
+                outputs=[2])[2]
+    parity("llm rmsnorm", got, oracle.rmsnorm(x, w, 1e-5, BC=bc))
+    idx = np.array([t - 1, 0, t // 2, 0], np.int32)
+    got = T.run("llm", "rmsnorm_rows", [x, idx, w, np.zeros((4, dm), np.float16)], [T.F32(1e-5)],
+                meta=[("BC", bc)], outputs=[3])[3]
+    parity("rmsnorm_rows", got, oracle.rmsnorm_rows(x, idx, w, 1e-5, BC=bc))
+    v = 300
+    e = r.tensor("f16", [v, dm])
+    tok = np.array([(i * 37) % v for i in range(t - 1)] + [v + 3], np.int32)
+    got = T.run("llm", "embed", [tok, e, np.zeros((t, dm), np.float32)], meta=[("BD", min(bc, 1024))],
+                outputs=[2])[2]
+    np.testing.assert_array_equal(got, oracle.embed(tok, e))
+
+
+@pytest.mark.parametrize("cfgname", ["tiny", "tinyllama"])
+def test_rope_and_kv_write(cfgname):
+    _say("rope/kv_write", cfgname)
+    cfg = getattr(oracle.Config, cfgname)()
+    c, s = oracle.rope_tables(cfg)
+    H, G, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+    Tn, W = 16, cfg.qkv()
+    r = oracle.Rng(13)
+    qkv = r.tensor("f16", [Tn, W])
+    pos = np.array([(i * 97) % cfg.max_pos for i in range(Tn)], np.int32)
+    q = T.run("llm", "rope_q", [qkv, pos, c, s, np.zeros((Tn, H, D), np.float16)], outputs=[4])[4]
+    want = oracle.rope_q(qkv, pos, c, s, H, D)
+    parity("rope_q", q, want)
+    assert np.abs(q.astype(np.float32) - want.astype(np.float32)).max() <= 2e-3 * max(1, np.abs(want).max())
+    NS = 40
+    slot = np.array([(i * 7) % NS for i in range(Tn - 2)] + [NS, -1], np.int32)  # last two dropped
+    Kc = r.tensor("f16", [NS, G, D])
+    Vc = r.tensor("f16", [NS, G, D])
+    K = np.zeros((Tn, G, D), np.float16)
+    V = np.zeros((Tn, G, D), np.float16)
+    out = T.run("llm", "kv_write", [qkv, pos, slot, c, s, Kc, Vc, K, V])
+    wKc, wVc, wK, wV = oracle.kv_write(qkv, pos, slot, c, s, Kc, Vc, K, V)
+    np.testing.assert_array_equal(out[6], wVc)  # values: copies, bit-exact
+    np.testing.assert_array_equal(out[8], wV)
+    parity("kv_write K", out[7], wK)
+    parity("kv_write Kc", out[5], wKc)
+    untouched = [i for i in range(NS) if i not in set(slot[:Tn - 2].tolist())]
+    np.testing.assert_array_equal(out[5][untouched], Kc[untouched])
