@@ -1,0 +1,296 @@
+"""Benchmark of tessel's kernel hot path on one MI355X.
+
+A step is one launch of the fp16 GEMM 4096x4096x4096 (BASELINE.json
+configs[1]; A, B ~ N(0,1)/sqrt(K) f16, f32 accumulation, f16 out), inputs
+resident in HBM. W untimed warm-up steps, then K steps timed with HIP
+events on the library's stream, bracketed by stream synchronisation.
+`value` is TFLOP/s (2MNK per step). The same JSON line carries:
+  roofline      the GEMM kernel's achieved TFLOP/s against the 2.5 PFLOP/s
+                fp16 dense MFMA peak; traffic = HBM bytes per launch from
+                the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summaries;
+  cpu_baseline  tessel's interpreter semantics (the oracle's C++
+                restatement) on a bounded sample of the same GEMM's programs;
+  cases         the other BASELINE configs measured the same way: GEMM
+                1024^3/2048^3, causal FlashAttention H32 D64 S 512..4096,
+                paged GQA decode (GB/s against 8 TB/s), RMSNorm and softmax
+                4096^2, and (--llm) TinyLlama-shape decode tokens/s.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_MFMA_F16 = 2500.0  # TFLOP/s, MI355X dense fp16
+PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def f16(a):
+    return np.ascontiguousarray(a, np.float16)
+
+
+class Timed:
+    """Event-timed launches of one kernel on the library stream."""
+
+    def __init__(self, T, k, args):
+        self.T, self.k, self.args = T, k, args
+
+    def warm(self, seconds=0.2, min_launches=3):
+        # At least 200 ms of launches, as src/runtime.rs:295-316 does, so the
+        # clocks have ramped up.
+        T = self.T
+        t0, n = time.perf_counter(), 0
+        while n < min_launches or time.perf_counter() - t0 < seconds:
+            T.launch(self.k, self.args)
+            n += 1
+            if n % 8 == 0:
+                T.sync()
+        T.sync()
+
+    def run(self, iters):
+        """Per-launch milliseconds over `iters` back-to-back launches."""
+        T = self.T
+        T.sync()
+        a = T.event_record()
+        for _ in range(iters):
+            T.launch(self.k, self.args)
+        b = T.event_record()
+        T.sync()
+        return T.event_elapsed(a, b) / iters
+
+    def median(self, iters, reps=5):
+        return float(np.median([self.run(iters) for _ in range(reps)]))
+
+
+def gemm_inputs(T, n, seed):
+    rng = np.random.default_rng(seed)
+    a = f16(rng.standard_normal((n, n), np.float32) / np.float32(np.sqrt(n)))
+    b = f16(rng.standard_normal((n, n), np.float32) / np.float32(np.sqrt(n)))
+    return a, b
+
+
+def gemm_case(T, n, seed=0):
+    a, b = gemm_inputs(T, n, seed)
+    bufs = [T.tensor(a), T.tensor(b), T.alloc(n * n * 2)]
+    k = T.kernel("matmul", "matmul", [[n, n]] * 3)
+    return Timed(T, k, bufs), 2.0 * n ** 3, (a, b)
+
+
+def load_traffic(name):
+    """HBM bytes per launch of a kernel, from the committed rocprofv3 PMC
+    summaries (profiles/traffic.json), or None."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(a, b, budget_s):
+    """The oracle (tessel's interpreter semantics restated in C++: f64 dot
+    products rounded per op, the f32 accumulator rounded per BK=32 tile,
+    BM=BN=128 programs) on a sample of the 4096^3 GEMM's 1024 programs,
+    growing until it has run for about budget_s seconds."""
+    import oracle
+
+    n = a.shape[0]
+    threads = min(os.cpu_count() or 1, 16)
+    per_prog = 2.0 * 128 * 128 * n
+    npids, spent, done = threads, 0.0, 0
+    c = np.zeros((n, n), np.float16)
+    while spent < budget_s and done < 1024:
+        npids = min(npids, 1024 - done)
+        t0 = time.perf_counter()
+        oracle.matmul(a, b, 128, 128, 32, 8, threads=threads, first_pid=done, npids=npids, C=c)
+        spent += time.perf_counter() - t0
+        done += npids
+        npids *= 2
+    tflops = per_prog * done / spent / 1e12
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of 1024 BM=BN=128 programs of the 4096^3 matmul (oracle, {threads} threads), "
+                      f"{spent:.1f} s"}
+
+
+def attention_case(T, s, seed=1):
+    rng = np.random.default_rng(seed)
+    h, d = 32, 64
+    q, k, v = (f16(rng.standard_normal((h, s, d), np.float32)) for _ in range(3))
+    bufs = [T.tensor(q), T.tensor(k), T.tensor(v), T.alloc(h * s * d * 2), T.F32(0.125)]
+    kern = T.kernel("attention", "flash_attention", [[h, s, d]] * 4)
+    return Timed(T, kern, bufs), 2.0 * h * s * s * d
+
+
+def decode_case(T, seed=2, b=64, h=32, g=8, d=128, p=16):
+    """lens ~ U[128, 4096], pages by seeded permutation."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(128, 4097, b).astype(np.int32)
+    need = (lens + p - 1) // p
+    mp = 256
+    npages = int(need.sum())
+    perm = rng.permutation(npages).astype(np.int32)
+    table = np.zeros((b, mp), np.int32)
+    o = 0
+    for i in range(b):
+        table[i, :need[i]] = perm[o:o + need[i]]
+        o += need[i]
+    q = f16(rng.standard_normal((b, h, d), np.float32))
+    kc = f16(rng.standard_normal((npages, p, g, d), np.float32))
+    vc = f16(rng.standard_normal((npages, p, g, d), np.float32))
+    bufs = [T.tensor(q), T.tensor(kc), T.tensor(vc), T.tensor(table), T.tensor(lens), T.alloc(b * h * d * 2),
+            T.F32(1.0 / np.sqrt(d))]
+    kern = T.kernel("llm", "decode_attention", [[b, h, d], [npages, p, g, d], [npages, p, g, d], [b, mp], [b],
+                                                [b, h, d]])
+    nbytes = float(lens.sum()) * g * d * 2 * 2 + b * h * d * 2 * 2 + 4 * b * mp + 4 * b
+    flops = 4.0 * float(lens.sum()) * h * d
+    return Timed(T, kern, bufs), nbytes, flops, int(lens.sum())
+
+
+def rows_case(T, kind):
+    rng = np.random.default_rng(3)
+    r = c = 4096
+    if kind == "softmax":
+        x = (rng.random((r, c), np.float32) * 8 - 4).astype(np.float32)
+        bufs = [T.tensor(x), T.alloc(r * c * 4)]
+        k = T.kernel("basic", "softmax", [[r, c]] * 2, [("BR", 1), ("BC", c)])
+        return Timed(T, k, bufs), 8.0 * r * c
+    x = f16(rng.random((r, c), np.float32) * 4 - 2)
+    w = f16(rng.random(c, np.float32) * 2 - 1)
+    bufs = [T.tensor(x), T.tensor(w), T.alloc(r * c * 2), T.F32(1e-5)]
+    k = T.kernel("basic", "rmsnorm", [[r, c], [c], [r, c]], [("BR", 1), ("BC", c)])
+    return Timed(T, k, bufs), 4.0 * r * c
+
+
+def llm_case(T, seqs=32, prompt=512, new=128):
+    """TinyLlama-1.1B shape, random fp16 weights, 32
+    prompts of 512 random ids, 128 greedy steps under continuous batching."""
+    cfg = T.Config.tinyllama()
+    t0 = time.perf_counter()
+    w = T.weights_random(cfg, 7)
+    lim = T.Limits(16, seqs * ((prompt + new + 15) // 16) + 64, 1024, (prompt + new + 15) // 16)
+    e = T.Engine(cfg, lim, w)
+    del w
+    rng = np.random.default_rng(5)
+    reqs = [(rng.integers(3, cfg.vocab, prompt).tolist(), new) for _ in range(seqs)]
+    # A short untimed run first: kernel specialisation, tuning, graph capture.
+    e.generate([(reqs[0][0][:64], 4)] * 2, seqs)
+    setup = time.perf_counter() - t0
+    outs, st = e.generate(reqs, seqs)
+    e.close()
+    return {"case": "llm_decode", "model": "TinyLlama-1.1B shape (random fp16 weights)",
+            "sequences": seqs, "prompt": prompt, "new_tokens": new,
+            "generated_tok_s": round(st.generated / st.seconds, 1),
+            "decode_tok_s": round(st.decode_tokens / st.decode_seconds, 1) if st.decode_seconds else None,
+            "seconds": round(st.seconds, 3), "decode_seconds": round(st.decode_seconds, 3),
+            "prefill_steps": st.prefill_steps, "decode_steps": st.decode_steps,
+            "largest_batch": st.largest_batch, "setup_s": round(setup, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cases", action="store_true", help="only the headline GEMM")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--llm", action="store_true", help="also run the TinyLlama decode case (config 5)")
+    ap.add_argument("--only", default="", help="comma list of cases (profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the kernels run on one MI355X; sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import tessel_amd as T
+
+    T.open()
+    cus, mhz = T.device_info()
+    log("device:", T.device_name(), cus, "CUs", mhz, "MHz")
+    only = set(filter(None, args.only.split(",")))
+
+    # ---- headline: GEMM 4096^3
+    g, flops, (a, b) = gemm_case(T, 4096)
+    g.warm()
+    for _ in range(args.warmup):
+        T.launch(g.k, g.args)
+    T.sync()
+    wall0 = time.perf_counter()
+    ms = g.run(args.steps)
+    wall = time.perf_counter() - wall0
+    value = flops / (ms * 1e-3) / 1e12
+    kern_ms = g.median(50)  # the kernel's average launch duration, for the roofline
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    traffic = load_traffic("matmul_4096")
+    line = {
+        "metric": "fp16 GEMM/attn TFLOP/s, paged-decode HBM GB/s, % of MI355X roofline",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "wall_s": round(wall, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16 (f32 accumulation)", "data": "synthetic",
+        "config": {"workload": "matmul 4096x4096x4096 (kernels/matmul.tl), A,B ~ N(0,1)/sqrt(K) f16",
+                   "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_MFMA_F16, 4), "traffic": traffic,
+                     "kernel": "gemm_f16<256,256,64,2,2> (matmul)", "kernel_ms": round(kern_ms, 5),
+                     "algorithmic_per_launch": "2MNK = 137.44 GFLOP"},
+        "device": {"name": T.device_name(), "cus": cus, "mhz": mhz},
+    }
+    cases = []
+    if not args.no_cases:
+        def want(n):
+            return not only or n in only
+
+        for n in (1024, 2048):
+            if not want(f"gemm{n}"):
+                continue
+            t, fl, _ = gemm_case(T, n, seed=n)
+            t.warm()
+            m = t.median(100)
+            cases.append({"case": f"gemm {n}^3", "ms": round(m, 5), "tflops": round(fl / m / 1e9, 2),
+                          "frac_mfma": round(fl / m / 1e9 / PEAK_MFMA_F16, 4)})
+        for s in (512, 1024, 2048, 4096):
+            if not want(f"fa{s}"):
+                continue
+            t, fl = attention_case(T, s)
+            t.warm()
+            m = t.median(50)
+            cases.append({"case": f"flash_attention H32 S{s} D64 causal", "ms": round(m, 5),
+                          "tflops": round(fl / m / 1e9, 2), "frac_mfma": round(fl / m / 1e9 / PEAK_MFMA_F16, 4)})
+        if want("decode"):
+            t, nb, fl, toks = decode_case(T)
+            t.warm()
+            m = t.median(50)
+            gbs = nb / m / 1e6
+            cases.append({"case": "decode_attention B64 H32 G8 D128 P16 ctx~U[128,4096]", "ms": round(m, 5),
+                          "gbps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4), "bytes": nb,
+                          "context_tokens": toks, "tflops": round(fl / m / 1e9, 3),
+                          "traffic": load_traffic("decode_attention")})
+        for kind in ("rmsnorm", "softmax"):
+            if not want(kind):
+                continue
+            t, nb = rows_case(T, kind)
+            t.warm()
+            m = t.median(50)
+            cases.append({"case": f"{kind} 4096x4096", "ms": round(m, 5), "gbps": round(nb / m / 1e6, 1),
+                          "frac_hbm": round(nb / m / 1e6 / PEAK_HBM, 4)})
+        if args.llm and want("llm"):
+            cases.append(llm_case(T))
+    if cases:
+        line["cases"] = cases
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(a, b, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -221,6 +221,212 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_f16(const u16* __restri
         }
 }
 
+// ---------------------------------------------------------------- the large-tile path
+// For K % 8 == 0 (and N % 8 == 0 when B is [K, N]): 256 x 256 x 64 tiles,
+// 4 wavefronts of 128 x 128. Tiles move global -> LDS with 16-byte buffer
+// loads that write LDS directly (no VGPR staging; lane i of a load lands at
+// the load's LDS base + 16 i, so the XOR swizzle is applied by choosing which
+// global chunk each lane fetches). Rows past M/N and k past K read as zero
+// (buffer range checking; a chunk past K is sent out of range explicitly).
+// A (and W [N, K]) is read as MFMA operands with ds_read_b128; B [K, N] stays
+// row-major in LDS and is read with ds_read_b64_tr_b16, which hands lane i
+// of each 16-lane group column n0 + i of 4 consecutive k rows: the B
+// operand's 8 k values per lane come from two such reads, no transpose pass.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_t;
+
+constexpr uint32_t RSRC_FLAGS = 0x00020000;  // gfx9 buffer resource word 3
+constexpr int OOB = 0x7fffffff;              // a byte offset past any range
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// A buffer resource (base, byte range, gfx9 flags) for buffer loads.
+TSL_DEV i32x4 make_rsrc(const void* p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    return i32x4{(int)(uint32_t)a, (int)(uint32_t)((a >> 32) & 0xffff), (int)bytes, (int)RSRC_FLAGS};
+}
+
+TSL_DEV half4 lds_read_tr(const u16* p) {
+    fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) fp16x4_t*)(p));
+    return __builtin_bit_cast(half4, v);
+}
+
+// The compute of a K step is software pipelined: the MFMA operands of
+// k-step s+1 are read from LDS while the 16 MFMAs of step s run.
+template <bool BT, int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_big(const u16* __restrict__ A, const u16* __restrict__ B,
+                                                   const u16* __restrict__ B2, void* __restrict__ C,
+                                                   const u16* __restrict__ bias, int M, int N, int K, int G) {
+    constexpr int BM = 256, BN = 256, BK = 64, KC = BK / 8;
+    constexpr int TM = 4, TN = 4;                 // 32x32 MFMA tiles per wave (128 x 128)
+    constexpr int STAGE = (BM + BN) * BK;         // halves per stage: A [256][64], then B
+    // B is [64][256] row-major (NN: 16-byte chunk p of row k XOR 2*(k%4)) or
+    // [256][64] like A (NT: chunk XOR row%8). Two stages of 64 KB.
+    __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm0 = (wave >> 1) * 128, wn0 = (wave & 1) * 128;
+    int tm, tn;
+    tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, (N + BN - 1) / BN, G, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int g = lane >> 5;
+
+    const i32x4 ra = make_rsrc(A, (uint32_t)((long)M * K * 2));
+    const i32x4 rb = make_rsrc(B, (uint32_t)((long)K * N * 2));
+    const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
+
+    // This wave's 16 loads per K step (8 for A, 8 for B), each filling 1 KB of
+    // the stage: byte offsets at k0 = 0 (OOB when the row is out of range).
+    // A load i: rows 64 wave + 8 i + lane/8, logical chunk (lane&7)^(lane>>3).
+    const int ca = (lane & 7) ^ (lane >> 3);
+    uint32_t offa[8], offb[8];
+    int rowb[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = 64 * wave + 8 * i + (lane >> 3);
+        offa[i] = m0 + r < M ? (uint32_t)(((m0 + r) * K + ca * 8) * 2) : (uint32_t)OOB;
+        if constexpr (BT) {
+            offb[i] = n0 + r < N ? (uint32_t)(((n0 + r) * K + ca * 8) * 2) : (uint32_t)OOB;
+            rowb[i] = 0;
+        } else {
+            const int rk = 16 * wave + 2 * i + (lane >> 5);             // k row of the tile
+            const int cb = (lane & 31) ^ (((2 * (i & 1) + (lane >> 5)) & 3) << 1);
+            const int n = n0 + cb * 8;
+            offb[i] = n < N ? (uint32_t)((rk * N + n) * 2) : (uint32_t)OOB;
+            rowb[i] = rk;
+        }
+    }
+    auto issue = [&](int k0, int stage) {
+        const uint32_t sa = lds_base + stage * STAGE * 2 + wave * 8 * 1024;
+        const uint32_t sb = lds_base + stage * STAGE * 2 + BM * BK * 2 + wave * 8 * 1024;
+        const bool ka = k0 + ca * 8 < K;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int v = (ka && offa[i] != (uint32_t)OOB) ? (int)(offa[i] + k0 * 2) : OOB;
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sa + i * 1024), "v"(v),
+                         "s"(ra));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            int v;
+            if constexpr (BT) v = (ka && offb[i] != (uint32_t)OOB) ? (int)(offb[i] + k0 * 2) : OOB;
+            else v = (k0 + rowb[i] < K && offb[i] != (uint32_t)OOB) ? (int)(offb[i] + k0 * N * 2) : OOB;
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sb + i * 1024), "v"(v),
+                         "s"(rb));
+        }
+    };
+
+    // LDS byte addresses of this lane's operands (stage 0): A at k-step s,
+    // tile i: a_addr[s] + 4096 i; B (NN) tile j: b_addr[j] + (16 s + 4 h) 512.
+    uint32_t a_addr[4], b_addr[4];
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+        const int r = wm0 + (lane & 31);
+        a_addr[st] = (uint32_t)((r * KC + ((2 * st + g) ^ (r & 7))) * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        if constexpr (BT) {
+            b_addr[j] = 0;
+        } else {
+            const int grp = lane >> 4, jj = lane & 15;
+            const int n = wn0 + j * 32 + 16 * (grp & 1) + 4 * (jj & 3);
+            const int k = 8 * g + (jj >> 2);
+            b_addr[j] = (uint32_t)(BM * BK * 2 + k * BN * 2 + ((((n >> 3) ^ ((k & 3) << 1)) << 3) + (n & 7)) * 2);
+        }
+    }
+    const char* ldsc = reinterpret_cast<const char*>(lds);
+    auto read_ops = [&](int stage_off, int st, half8* av, half8* bv) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+            av[i] = *reinterpret_cast<const half8*>(ldsc + stage_off + a_addr[st] + i * 4096);
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            if constexpr (BT) {
+                const int r = wn0 + j * 32 + (lane & 31);
+                bv[j] = *reinterpret_cast<const half8*>(ldsc + stage_off + BM * BK * 2 +
+                                                        (r * KC + ((2 * st + g) ^ (r & 7))) * 16);
+            } else {
+                const half4 h0 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + stage_off + b_addr[j] + (16 * st) * BN * 2));
+                const half4 h1 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + stage_off + b_addr[j] + (16 * st + 4) * BN * 2));
+                bv[j] = half8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+            }
+        }
+    };
+
+    float16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = float16v{};
+
+    const int nk = (K + BK - 1) / BK;
+    issue(0, 0);
+    for (int kt = 0; kt < nk; kt++) {
+        const int stage = kt & 1;
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of step kt are in LDS
+        __syncthreads();                     // everyone's; and step kt-1 is done reading the other stage
+        if (kt + 1 < nk) issue((kt + 1) * BK, stage ^ 1);
+        const int so = stage * STAGE * 2;
+        half8 a0[TM], b0[TN], a1[TM], b1[TN];
+        read_ops(so, 0, a0, b0);
+#pragma unroll
+        for (int st = 0; st < BK / 16; st++) {
+            half8* av = (st & 1) ? a1 : a0;
+            half8* bv = (st & 1) ? b1 : b0;
+            if (st + 1 < BK / 16) read_ops(so, st + 1, (st & 1) ? a0 : a1, (st & 1) ? b0 : b1);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+        // Pin the schedule: step 0's operand reads, then per k-step the next
+        // step's reads spread over its first MFMAs, the rest back to back.
+        constexpr int NRD = BT ? TM + TN : TM + 2 * TN;  // LDS reads per k-step
+        __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
+#pragma unroll
+        for (int st = 0; st < BK / 16; st++) {
+            if (st + 1 < BK / 16) {
+#pragma unroll
+                for (int t = 0; t < NRD / 2; t++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - NRD / 2, 0);
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int col = n0 + wn0 + j * 32 + (lane & 31);
+            if (col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (row >= M) continue;
+                const size_t o = (size_t)row * N + col;
+                const float v = acc[i][j][r];
+                if constexpr (EPI == EPI_F16) {
+                    reinterpret_cast<u16*>(C)[o] = f2h(v);
+                } else if constexpr (EPI == EPI_F32) {
+                    reinterpret_cast<float*>(C)[o] = v;
+                } else if constexpr (EPI == EPI_RESID) {
+                    float* R = reinterpret_cast<float*>(C);
+                    R[o] = R[o] + v;
+                } else {
+                    reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
+                }
+            }
+        }
+}
+
 // matmul_f32 (kernels/matmul.tl:19-27): f32 operands through LDS, f32 FMA.
 __global__ __launch_bounds__(256) void matmul_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                          float* __restrict__ C, int M, int N, int K) {
@@ -265,6 +471,13 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     constexpr bool DUAL = EPI == EPI_SWIGLU;
     if constexpr (!DUAL) {
+        const bool aligned = (K % 8) == 0 && (BT || (N % 8) == 0) && (long)M * K < (1L << 30) &&
+                             (long)N * K < (1L << 30);
+        if (tiles(256, 256) >= 224 && aligned) {
+            hipLaunchKernelGGL((gemm_big<BT, EPI>), dim3(tiles(256, 256)), dim3(256), 0, s, A, B, B2, C, bias, M, N,
+                               K, 4);
+            return TSL_LAUNCHED(what);
+        }
         if (tiles(256, 256) >= 224) return run_gemm<256, 256, 64, 2, 2, BT, EPI>(A, B, B2, C, bias, M, N, K, s, what);
     }
     if (tiles(128, 128) >= 224 || M > 64) return run_gemm<128, 128, 64, 2, 2, BT, EPI>(A, B, B2, C, bias, M, N, K, s, what);
