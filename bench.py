@@ -46,6 +46,9 @@ class Timed:
         self.T, self.k, self.args = T, k, args
 
     def warm(self, seconds=0.2, min_launches=3):
+        self._warm(seconds, min_launches)
+
+    def _warm(self, seconds, min_launches):
         # At least 200 ms of launches, as src/runtime.rs:295-316 does, so the
         # clocks have ramped up.
         T = self.T
@@ -205,7 +208,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--llm", action="store_true", help="also run the TinyLlama decode case (config 5)")
-    ap.add_argument("--only", default="", help="comma list of cases (profiling runs)")
+    ap.add_argument("--only", default="", help="comma list of cases: gemm1024,gemm2048,fa512..fa4096,decode,"
+                    "rmsnorm,softmax,llm; 'none' for the headline GEMM alone")
+    ap.add_argument("--profile", action="store_true",
+                    help="few launches, no clock warm-up: for rocprofv3 counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -220,6 +226,9 @@ def main():
     only = set(filter(None, args.only.split(",")))
 
     # ---- headline: GEMM 4096^3
+    if args.profile:
+        Timed.warm = lambda self, seconds=0.0, min_launches=2: Timed._warm(self, seconds, min_launches)
+        Timed.median = lambda self, iters, reps=1: Timed.run(self, min(iters, 5))
     g, flops, (a, b) = gemm_case(T, 4096)
     g.warm()
     for _ in range(args.warmup):

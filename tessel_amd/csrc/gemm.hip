@@ -223,7 +223,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_f16(const u16* __restri
 
 // ---------------------------------------------------------------- the large-tile path
 // For K % 8 == 0 (and N % 8 == 0 when B is [K, N]): 256 x 256 x 64 tiles,
-// 4 wavefronts of 128 x 128. Tiles move global -> LDS with 16-byte buffer
+// 8 wavefronts of 128 x 64. Tiles move global -> LDS with 16-byte buffer
 // loads that write LDS directly (no VGPR staging; lane i of a load lands at
 // the load's LDS base + 16 i, so the XOR swizzle is applied by choosing which
 // global chunk each lane fetches). Rows past M/N and k past K read as zero
@@ -253,104 +253,133 @@ TSL_DEV half4 lds_read_tr(const u16* p) {
 
 // The compute of a K step is software pipelined: the MFMA operands of
 // k-step s+1 are read from LDS while the 16 MFMAs of step s run.
-template <bool BT, int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_big(const u16* __restrict__ A, const u16* __restrict__ B,
-                                                   const u16* __restrict__ B2, void* __restrict__ C,
-                                                   const u16* __restrict__ bias, int M, int N, int K, int G) {
-    constexpr int BM = 256, BN = 256, BK = 64, KC = BK / 8;
-    constexpr int TM = 4, TN = 4;                 // 32x32 MFMA tiles per wave (128 x 128)
-    constexpr int STAGE = (BM + BN) * BK;         // halves per stage: A [256][64], then B
-    // B is [64][256] row-major (NN: 16-byte chunk p of row k XOR 2*(k%4)) or
-    // [256][64] like A (NT: chunk XOR row%8). Two stages of 64 KB.
-    __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE];
+//
+// LDS is served 16 lanes per cycle for 16-byte reads and 32 lanes for 8-byte
+// ones, so the swizzles keep every such lane group on distinct banks: A row r
+// holds logical chunk c at chunk c ^ ((r >> 1) & 7) (16 consecutive rows of an
+// operand read cover all 16 slots of the 256-byte bank window); B row k (NN)
+// holds logical chunk c at c ^ ((k & 3) << 2), so the 4 k rows x 2 column
+// halves a 32-lane transposed read touches are 8 distinct 32-byte granules.
+template <bool BT, int EPI, int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restrict__ A, const u16* __restrict__ B,
+                                                             const u16* __restrict__ B2, void* __restrict__ C,
+                                                             const u16* __restrict__ bias, int M, int N, int K,
+                                                             int G) {
+    constexpr int BK = 64, KC = BK / 8;
+    constexpr int NW = WGM * WGN;                 // wavefronts: WGM x WGN, each (BM/WGM) x (BN/WGN)
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TM = WM / 32, TN = WN / 32;     // 32x32 MFMA tiles per wave
+    constexpr int LPA = BM / 8 / NW, LPB = BN / 8 / NW;  // 1 KB loads per wave per K step
+    constexpr int RPL = 512 / BN;                 // B [K, N] rows per 1 KB load
+    static_assert(TM >= 1 && TN >= 1 && LPA >= 1 && LPB >= 1 && (BT || BN >= 128), "tile shape");
+    constexpr int STAGE = (BM + BN) * BK * 2;     // bytes per stage: A [BM][64], then B
+    __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE / 2];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm0 = (wave >> 1) * 128, wn0 = (wave & 1) * 128;
+    const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
     int tm, tn;
     tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, (N + BN - 1) / BN, G, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int g = lane >> 5;
-
-    const i32x4 ra = make_rsrc(A, (uint32_t)((long)M * K * 2));
-    const i32x4 rb = make_rsrc(B, (uint32_t)((long)K * N * 2));
     const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
 
-    // This wave's 16 loads per K step (8 for A, 8 for B), each filling 1 KB of
-    // the stage: byte offsets at k0 = 0 (OOB when the row is out of range).
-    // A load i: rows 64 wave + 8 i + lane/8, logical chunk (lane&7)^(lane>>3).
-    const int ca = (lane & 7) ^ (lane >> 3);
-    uint32_t offa[8], offb[8];
-    int rowb[8];
+    // This wave's LPA + LPB loads per K step (for A, then B), each filling 1 KB of
+    // a stage. Per-lane byte offsets are relative to the K step's first
+    // column (A, W) or row (B): the buffer base advances with k instead, in
+    // scalar registers. OOB marks a row or column outside the matrix.
+    uint32_t offa[LPA], offb[LPB];
+    int ka[LPA], kb[LPB];  // the k this lane's chunk starts at, within the step (for a partial last step)
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int r = 64 * wave + 8 * i + (lane >> 3);
-        offa[i] = m0 + r < M ? (uint32_t)(((m0 + r) * K + ca * 8) * 2) : (uint32_t)OOB;
+    for (int i = 0; i < LPA; i++) {
+        const int q = wave * LPA + i;
+        const int r = 8 * q + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        ka[i] = 8 * c;
+        offa[i] = m0 + r < M ? (uint32_t)(((m0 + r) * K + 8 * c) * 2) : (uint32_t)OOB;
+    }
+#pragma unroll
+    for (int i = 0; i < LPB; i++) {
+        const int q = wave * LPB + i;
         if constexpr (BT) {
-            offb[i] = n0 + r < N ? (uint32_t)(((n0 + r) * K + ca * 8) * 2) : (uint32_t)OOB;
-            rowb[i] = 0;
+            const int r = 8 * q + (lane >> 3);
+            const int c = (lane & 7) ^ ((r >> 1) & 7);
+            kb[i] = 8 * c;
+            offb[i] = n0 + r < N ? (uint32_t)(((n0 + r) * K + 8 * c) * 2) : (uint32_t)OOB;
         } else {
-            const int rk = 16 * wave + 2 * i + (lane >> 5);             // k row of the tile
-            const int cb = (lane & 31) ^ (((2 * (i & 1) + (lane >> 5)) & 3) << 1);
-            const int n = n0 + cb * 8;
+            const int rk = RPL * q + lane / (BN / 8);  // k row of the step
+            const int cb = (lane % (BN / 8)) ^ ((rk & 3) << 2);
+            const int n = n0 + 8 * cb;
+            kb[i] = rk;
             offb[i] = n < N ? (uint32_t)((rk * N + n) * 2) : (uint32_t)OOB;
-            rowb[i] = rk;
         }
     }
     auto issue = [&](int k0, int stage) {
-        const uint32_t sa = lds_base + stage * STAGE * 2 + wave * 8 * 1024;
-        const uint32_t sb = lds_base + stage * STAGE * 2 + BM * BK * 2 + wave * 8 * 1024;
-        const bool ka = k0 + ca * 8 < K;
+        // Resources whose base is the step's first column (A) / row (B).
+        const long a_shift = (long)k0 * 2, b_shift = BT ? (long)k0 * 2 : (long)k0 * N * 2;
+        const i32x4 ra = make_rsrc(reinterpret_cast<const char*>(A) + a_shift, (uint32_t)((long)M * K * 2 - a_shift));
+        const i32x4 rb = make_rsrc(reinterpret_cast<const char*>(B) + b_shift,
+                                   (uint32_t)((BT ? (long)N * K : (long)K * N) * 2 - b_shift));
+        const uint32_t sa = lds_base + stage * STAGE + wave * LPA * 1024;
+        const uint32_t sb = lds_base + stage * STAGE + BM * BK * 2 + wave * LPB * 1024;
+        if (k0 + BK <= K) {  // every k of the step exists (uniform)
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int v = (ka && offa[i] != (uint32_t)OOB) ? (int)(offa[i] + k0 * 2) : OOB;
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sa + i * 1024), "v"(v),
-                         "s"(ra));
-        }
+            for (int i = 0; i < LPA; i++)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sa + i * 1024),
+                             "v"(offa[i]), "s"(ra));
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            int v;
-            if constexpr (BT) v = (ka && offb[i] != (uint32_t)OOB) ? (int)(offb[i] + k0 * 2) : OOB;
-            else v = (k0 + rowb[i] < K && offb[i] != (uint32_t)OOB) ? (int)(offb[i] + k0 * N * 2) : OOB;
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sb + i * 1024), "v"(v),
-                         "s"(rb));
+            for (int i = 0; i < LPB; i++)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sb + i * 1024),
+                             "v"(offb[i]), "s"(rb));
+        } else {
+#pragma unroll
+            for (int i = 0; i < LPA; i++) {
+                const uint32_t v = k0 + ka[i] < K ? offa[i] : (uint32_t)OOB;
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sa + i * 1024),
+                             "v"(v), "s"(ra));
+            }
+#pragma unroll
+            for (int i = 0; i < LPB; i++) {
+                const uint32_t v = k0 + kb[i] < K ? offb[i] : (uint32_t)OOB;
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sb + i * 1024),
+                             "v"(v), "s"(rb));
+            }
         }
     };
 
-    // LDS byte addresses of this lane's operands (stage 0): A at k-step s,
+    // LDS byte addresses of this lane's operands in stage 0: A at k-step s,
     // tile i: a_addr[s] + 4096 i; B (NN) tile j: b_addr[j] + (16 s + 4 h) 512.
-    uint32_t a_addr[4], b_addr[4];
+    uint32_t a_addr[4], b_addr[TN];
 #pragma unroll
     for (int st = 0; st < 4; st++) {
         const int r = wm0 + (lane & 31);
-        a_addr[st] = (uint32_t)((r * KC + ((2 * st + g) ^ (r & 7))) * 16);
+        a_addr[st] = (uint32_t)((r * KC + ((2 * st + g) ^ ((r >> 1) & 7))) * 16);
     }
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         if constexpr (BT) {
-            b_addr[j] = 0;
+            const int r = wn0 + j * 32 + (lane & 31);
+            b_addr[j] = (uint32_t)(BM * BK * 2 + r * KC * 16);
         } else {
             const int grp = lane >> 4, jj = lane & 15;
             const int n = wn0 + j * 32 + 16 * (grp & 1) + 4 * (jj & 3);
             const int k = 8 * g + (jj >> 2);
-            b_addr[j] = (uint32_t)(BM * BK * 2 + k * BN * 2 + ((((n >> 3) ^ ((k & 3) << 1)) << 3) + (n & 7)) * 2);
+            b_addr[j] = (uint32_t)(BM * BK * 2 + k * BN * 2 + ((((n >> 3) ^ ((k & 3) << 2)) << 3) + (n & 7)) * 2);
         }
     }
     const char* ldsc = reinterpret_cast<const char*>(lds);
-    auto read_ops = [&](int stage_off, int st, half8* av, half8* bv) {
+    auto read_ops = [&](int so, int st, half8* av, half8* bv) {
 #pragma unroll
-        for (int i = 0; i < TM; i++)
-            av[i] = *reinterpret_cast<const half8*>(ldsc + stage_off + a_addr[st] + i * 4096);
+        for (int i = 0; i < TM; i++) av[i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 4096);
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             if constexpr (BT) {
                 const int r = wn0 + j * 32 + (lane & 31);
-                bv[j] = *reinterpret_cast<const half8*>(ldsc + stage_off + BM * BK * 2 +
-                                                        (r * KC + ((2 * st + g) ^ (r & 7))) * 16);
+                bv[j] = *reinterpret_cast<const half8*>(ldsc + so + b_addr[j] + (((2 * st + g) ^ ((r >> 1) & 7)) * 16));
             } else {
-                const half4 h0 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + stage_off + b_addr[j] + (16 * st) * BN * 2));
-                const half4 h1 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + stage_off + b_addr[j] + (16 * st + 4) * BN * 2));
-                bv[j] = half8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+                const half4 h0 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + (16 * st) * BN * 2));
+                const half4 h1 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + (16 * st + 4) * BN * 2));
+                bv[j] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
             }
         }
     };
@@ -363,13 +392,13 @@ __global__ __launch_bounds__(256, 1) void gemm_big(const u16* __restrict__ A, co
 
     const int nk = (K + BK - 1) / BK;
     issue(0, 0);
+    half8 a0[TM], b0[TN], a1[TM], b1[TN];
     for (int kt = 0; kt < nk; kt++) {
         const int stage = kt & 1;
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of step kt are in LDS
         __syncthreads();                     // everyone's; and step kt-1 is done reading the other stage
         if (kt + 1 < nk) issue((kt + 1) * BK, stage ^ 1);
-        const int so = stage * STAGE * 2;
-        half8 a0[TM], b0[TN], a1[TM], b1[TN];
+        const int so = stage * STAGE;
         read_ops(so, 0, a0, b0);
 #pragma unroll
         for (int st = 0; st < BK / 16; st++) {
@@ -474,8 +503,15 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
         const bool aligned = (K % 8) == 0 && (BT || (N % 8) == 0) && (long)M * K < (1L << 30) &&
                              (long)N * K < (1L << 30);
         if (tiles(256, 256) >= 224 && aligned) {
-            hipLaunchKernelGGL((gemm_big<BT, EPI>), dim3(tiles(256, 256)), dim3(256), 0, s, A, B, B2, C, bias, M, N,
-                               K, 4);
+            // 8 wavefronts of 128 x 64 (2 per SIMD, 128 accumulator registers
+            // each): one wave's MFMAs cover the other's loads and barrier.
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, B2,
+                               C, bias, M, N, K, 4);
+            return TSL_LAUNCHED(what);
+        }
+        if (aligned && M > 64) {
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
+                               C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
         if (tiles(256, 256) >= 224) return run_gemm<256, 256, 64, 2, 2, BT, EPI>(A, B, B2, C, bias, M, N, K, s, what);
