@@ -6,14 +6,14 @@
 //
 // A workgroup of 4 wavefronts owns 128 query rows of one head; each
 // wavefront owns 32. Per block of 64 keys, staged in LDS (double-buffered
-// through registers):
+// by direct loads that overlap the previous block's compute):
 //   S^T = K Q^T     (v_mfma_f32_32x32x16_f16; lane l holds query l % 32,
 //                    so the online-softmax state is per lane)
 //   O^T += V^T P^T  (P^T taken straight from the S^T accumulators, rounded
 //                    to f16 as the .tl's f16(p) does)
-// K is staged row-major ([key][d], 16-byte chunks XOR-swizzled); V is
-// staged transposed ([d][key]) by 4x4 register transposes so that the V^T
-// operand reads 4 consecutive keys per 8-byte LDS read. The key order
+// K and V are staged row-major ([key][d], 16-byte chunks XOR-swizzled) by
+// direct buffer->LDS loads; the V^T operand comes from transposed LDS reads
+// (ds_read_b64_tr_b16), 4 keys of one d column per lane. The key order
 // inside a 16-key MFMA step is permuted identically for P^T and V^T (the
 // reduction does not depend on it). exp is exp2 with log2(e) folded into
 // the scale. Query blocks are issued longest (most keys) first.
@@ -35,18 +35,53 @@ struct AttnArgs {
     float scale;
 };
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_t;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+TSL_DEV i32x4 make_rsrc(const void* p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    return i32x4{(int)(uint32_t)a, (int)(uint32_t)((a >> 32) & 0xffff), (int)bytes, 0x00020000};
+}
+
+TSL_DEV half4 lds_read_tr(const void* p) {
+    fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) fp16x4_t*)(p));
+    return __builtin_bit_cast(half4, v);
+}
+
+// LDS layouts of a 64-key block (K then V, each [64][D] row-major, 2D bytes
+// a row) with 16-byte-chunk XOR swizzles chosen so that the lane groups LDS
+// serves together (16 lanes of a 16-byte read, 32 of an 8-byte transposed
+// read) fall on distinct banks of the 256-byte bank window:
+//   K: 16 consecutive keys read the same logical chunk -> chunk ^ ((key / (128/D)) % (D/8))
+//   V: 4 key rows x 32 d of a transposed read -> 32-byte granule ^ 2*((row>>1)&1)
+//      (D = 64) or 2*(row&3) (D = 128); D <= 32 needs none.
+template <int D>
+TSL_DEV int swz_k(int key) {
+    constexpr int KCH = D / 8, RPW = D >= 128 ? 1 : 128 / D;
+    return (key / RPW) & (KCH - 1);
+}
+template <int D>
+TSL_DEV int swz_v(int key) {  // in 16-byte chunks
+    if constexpr (D == 64) return 4 * ((key >> 1) & 1);
+    else if constexpr (D == 128) return 4 * (key & 3);
+    else return 0;
+}
+
 template <int D, bool PREFILL>
 __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
-    constexpr int DP = D < 32 ? 32 : D;   // V^T rows, padded to one MFMA tile
-    constexpr int KCH = D / 8;            // 16-byte chunks per K row
-    constexpr int NVB = (BKEY / 4) * (D / 4);  // 4x4 blocks of a V tile
-    constexpr int VPT = (NVB + 255) / 256;
-    constexpr int KPT = (BKEY * KCH + 255) / 256;
+    constexpr int DP = D < 32 ? 32 : D;     // V^T rows, padded to one MFMA tile
+    constexpr int KCH = D / 8;              // 16-byte chunks per row
+    constexpr int ROWB = 2 * D;             // bytes per K or V row
+    constexpr int KPL = 1024 / ROWB;        // rows per 1 KB load
+    constexpr int NL = BKEY / KPL;          // 1 KB loads per matrix per block
+    constexpr int LPW = NL >= 4 ? NL / 4 : 1;  // loads per wave per matrix (waves >= NL idle when NL < 4)
+    constexpr int STAGE = 2 * BKEY * ROWB;  // K then V
+    constexpr float LAZY = 8.0f;            // rescale only when the max grows by more than 2^8
+    __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
 
-    __shared__ u32x4 lds_k[2][BKEY * KCH];
-    __shared__ u32x2 lds_v[2][DP * (BKEY / 4)];  // [d][key/4] 8-byte chunks
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g4 = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nqb = (a.S + BQ - 1) / BQ;
     const int qb = nqb - 1 - (int)(blockIdx.x / a.H);
     const int h = blockIdx.x % a.H;
@@ -55,8 +90,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     const int myq = qw + (lane & 31);
 
     const u16* Qh = a.Q + (long)h * a.q_head;
-    const u16* Kh = a.K + (long)hk * a.k_head;
-    const u16* Vh = a.V + (long)hk * a.k_head;
+    const char* Kh = reinterpret_cast<const char*>(a.K + (long)hk * a.k_head);
+    const char* Vh = reinterpret_cast<const char*>(a.V + (long)hk * a.k_head);
+    const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
 
     // Q^T operand, kept in registers: lane l holds d = 16 s + 8 (l/32) .. +8 of its query.
     half8 qop[D / 16];
@@ -69,163 +105,167 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     const int my_start = PREFILL ? (myq < a.S ? a.starts[myq] : 0) : 0;
     const float c2 = a.scale * LOG2E;
 
-    float m = PREFILL ? -1e30f * LOG2E : -INFINITY;  // running max, log2 domain
+    // This lane's byte offsets (relative to the block's first key row) for the
+    // wave's K and V loads; the buffer base advances with the block.
+    uint32_t offk[LPW], offv[LPW];
+    bool ldk[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; i++) {
+        const int q = wave * LPW + i;
+        const int key = q * KPL + lane / KCH, p = lane % KCH;
+        ldk[i] = q < NL;
+        offk[i] = (uint32_t)(key * a.k_row * 2 + ((p ^ swz_k<D>(key)) * 16));
+        offv[i] = (uint32_t)(key * a.k_row * 2 + ((p ^ swz_v<D>(key)) * 16));
+    }
+    auto issue = [&](int j, int stage) {
+        const long shift = (long)j * a.k_row * 2;
+        const uint32_t range = (uint32_t)(((long)a.S - j) * a.k_row * 2);
+        const i32x4 rk = make_rsrc(Kh + shift, range), rv = make_rsrc(Vh + shift, range);
+        const uint32_t sk = lds_base + stage * STAGE + wave * LPW * 1024, sv = sk + BKEY * ROWB;
+#pragma unroll
+        for (int i = 0; i < LPW; i++) {
+            if (!ldk[i]) continue;  // wave-uniform
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sk + i * 1024),
+                         "v"(offk[i]), "s"(rk));
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sv + i * 1024),
+                         "v"(offv[i]), "s"(rv));
+        }
+    };
+
+    // Operand addresses within a stage. K (A operand of S^T): key kt*32 + l%32,
+    // logical chunk 2 s + g. V^T (A operand of O^T) by transposed reads:
+    // provider (grp, jj) points at key row 16 t + 8 h + 4 g + jj/4 and
+    // columns dt*32 + 16 (grp&1) + 4 (jj&3) .. +3, so lane l receives column
+    // dt*32 + l%32 for keys 16 t + 8 h + 4 g + 0..3, the key order the P^T
+    // operand (the S^T accumulator) has.
+    const int grp = lane >> 4, jj = lane & 15;
+    uint32_t kaddr[2][D / 16];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int s = 0; s < D / 16; s++) {
+            const int key = kt * 32 + (lane & 31);
+            kaddr[kt][s] = (uint32_t)(key * ROWB + (((2 * s + g4) ^ swz_k<D>(key)) * 16));
+        }
+    uint32_t vaddr[DP / 32];
+    const int vrow0 = 4 * g4 + (jj >> 2);  // + 16 t + 8 h
+#pragma unroll
+    for (int dt = 0; dt < DP / 32; dt++) {
+        const int d = dt * 32 + 16 * (grp & 1) + 4 * (jj & 3);
+        const int dd = d < D ? d : 0;
+        vaddr[dt] = (uint32_t)(BKEY * ROWB + vrow0 * ROWB + ((((dd >> 3) ^ swz_v<D>(vrow0)) << 4) + (dd & 7) * 2));
+    }
+
+    float m = PREFILL ? -1e30f : -INFINITY;  // running max of raw scores
+    float mc = PREFILL ? -1e30f * c2 : -INFINITY;  // the same, times c2
     float lsum = 0.0f;
     float16v acc[DP / 32];
 #pragma unroll
     for (int i = 0; i < DP / 32; i++) acc[i] = float16v{};
+    const half2v ones = {(half_t)1.0f, (half_t)1.0f};
 
     const int kend = min(q0 + BQ, a.S);
-    int kbeg = 0;
-    if (PREFILL) kbeg = (a.starts[q0] / BKEY) * BKEY;
-
-    u32x4 rk[KPT > 0 ? KPT : 1];
-    u32x2 rv[VPT][4];
-    auto gload = [&](int j) {
-#pragma unroll
-        for (int i = 0; i < KPT; i++) {
-            int c = tid + i * 256;
-            int key = c / KCH, ch = c % KCH;
-            u32x4 t = {0, 0, 0, 0};
-            if (c < BKEY * KCH && j + key < a.S)
-                t = *reinterpret_cast<const u32x4*>(Kh + (long)(j + key) * a.k_row + ch * 8);
-            rk[i] = t;
-        }
-#pragma unroll
-        for (int i = 0; i < VPT; i++) {
-            int b = tid + i * 256;
-            int kg = b / (D / 4), dg = b % (D / 4);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                int key = j + kg * 4 + r;
-                u32x2 t = {0, 0};
-                if (b < NVB && key < a.S) t = *reinterpret_cast<const u32x2*>(Vh + (long)key * a.k_row + dg * 4);
-                rv[i][r] = t;
-            }
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < KPT; i++) {
-            int c = tid + i * 256;
-            if (c >= BKEY * KCH) break;
-            int key = c / KCH, ch = c % KCH;
-            lds_k[buf][key * KCH + (ch ^ ((key ^ (key >> 3)) & (KCH - 1)))] = rk[i];
-        }
-#pragma unroll
-        for (int i = 0; i < VPT; i++) {
-            int b = tid + i * 256;
-            if (b >= NVB) break;
-            int kg = b / (D / 4), dg = b % (D / 4);
-#pragma unroll
-            for (int c = 0; c < 4; c++) {  // d = 4 dg + c: keys 4 kg .. 4 kg + 3
-                uint32_t w0 = c < 2 ? rv[i][0][0] : rv[i][0][1], w1 = c < 2 ? rv[i][1][0] : rv[i][1][1];
-                uint32_t w2 = c < 2 ? rv[i][2][0] : rv[i][2][1], w3 = c < 2 ? rv[i][3][0] : rv[i][3][1];
-                uint32_t lo, hi;
-                if (c & 1) {
-                    lo = (w0 >> 16) | (w1 & 0xffff0000u);
-                    hi = (w2 >> 16) | (w3 & 0xffff0000u);
-                } else {
-                    lo = (w0 & 0xffffu) | (w1 << 16);
-                    hi = (w2 & 0xffffu) | (w3 << 16);
-                }
-                int d = dg * 4 + c;
-                lds_v[buf][d * (BKEY / 4) + (kg ^ (d & 15))] = u32x2{lo, hi};
-            }
-        }
-        if constexpr (D < 32) {  // zero V^T rows D .. 31 (read by the padded tile)
-            for (int e = tid; e < (DP - D) * (BKEY / 4); e += 256) lds_v[buf][D * (BKEY / 4) + e] = u32x2{0, 0};
-        }
-    };
-
-    if (kbeg < kend) {
-        gload(kbeg);
-        sstore(0);
-    }
-    __syncthreads();
-    int it = 0;
-    for (int j = kbeg; j < kend; j += BKEY, it++) {
-        const int buf = it & 1;
-        if (j + BKEY < kend) gload(j + BKEY);
+    const int kbeg = PREFILL ? (a.starts[q0] / BKEY) * BKEY : 0;
+    const int nblk = kbeg < kend ? (kend - kbeg + BKEY - 1) / BKEY : 0;
+    if (nblk > 0) issue(kbeg, 0);
+    for (int b = 0; b < nblk; b++) {
+        const int j = kbeg + b * BKEY;
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of block b are in LDS
+        __syncthreads();                     // everyone's; and block b-1's reads of the other stage are done
+        if (b + 1 < nblk) issue(j + BKEY, (b + 1) & 1);
+        const char* st_base = lds + (b & 1) * STAGE;
         const bool active = j <= qw + 31 && qw < a.S;  // some key of this block <= some query of the wave
-        if (active) {
-            float16v st[2];
+        if (!active) continue;
+        // S^T = K Q^T for the 64 keys x this wave's 32 queries (two 32-key tiles).
+        float16v st[2];
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-                st[kt] = float16v{};
-                const int key = kt * 32 + (lane & 31);
+        for (int kt = 0; kt < 2; kt++) {
+            st[kt] = float16v{};
 #pragma unroll
-                for (int s = 0; s < D / 16; s++) {
-                    const int ch = 2 * s + g4;
-                    half8 kop = __builtin_bit_cast(half8, lds_k[buf][key * KCH + (ch ^ ((key ^ (key >> 3)) & (KCH - 1)))]);
-                    st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[s], st[kt], 0, 0, 0);
-                }
+            for (int s = 0; s < D / 16; s++) {
+                const half8 kop = *reinterpret_cast<const half8*>(st_base + kaddr[kt][s]);
+                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[s], st[kt], 0, 0, 0);
             }
-            const bool need_mask = PREFILL || j + BKEY - 1 > qw || j + BKEY > a.S;
-            float mb = -INFINITY;
+        }
+        // Keys masked off: above the diagonal, past S and (prefill) before the
+        // row's own start. Key = j + 4 g + off_r with off_r a constant of the
+        // register, so each test is one compare against a per-lane limit.
+        if (PREFILL || j + BKEY - 1 > qw || j + BKEY > a.S) {
+            const int hi_lim = min(myq, a.S - 1) - j - 4 * g4;  // keep off_r <= hi_lim
+            const int lo_lim = PREFILL ? my_start - j - 4 * g4 : -(1 << 30);  // keep off_r >= lo_lim
 #pragma unroll
             for (int kt = 0; kt < 2; kt++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    float v = st[kt][r] * c2;
-                    if (need_mask) {
-                        const int key = j + kt * 32 + 8 * (r >> 2) + 4 * g4 + (r & 3);
-                        bool keep = key <= myq && key < a.S;
-                        if (PREFILL) keep = keep && key >= my_start;
-                        v = keep ? v : -INFINITY;
-                    }
-                    st[kt][r] = v;
-                    mb = fmaxf(mb, v);
+                    const int off = kt * 32 + 8 * (r >> 2) + (r & 3);
+                    bool keep = off <= hi_lim;
+                    if (PREFILL) keep = keep && off >= lo_lim;
+                    st[kt][r] = keep ? st[kt][r] : -INFINITY;
                 }
-            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        }
+        float mb = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) mb = fmaxf(mb, st[kt][r]);
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        // Lazy rescaling: the running max moves only when it would grow by
+        // more than 2^LAZY (p stays <= 2^LAZY meanwhile; acc / l does not
+        // depend on which max was used).
+        const bool grow = mb * c2 > mc + LAZY;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
             const float mn = fmaxf(m, mb);
-            const float alpha = __builtin_amdgcn_exp2f(m - mn);
-            float ps = 0.0f;
-            half8 pk[4];
+            const float mcn = mn * c2;
+            const float alpha = __builtin_amdgcn_exp2f(mc - mcn);
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DP / 32; dt++) acc[dt] *= alpha;
+            m = mn;
+            mc = mcn;
+        }
+        // P = exp2(s c2 - m c2), rounded to f16 as the .tl's f16(p); row sums
+        // from the f16 pairs. Then O^T += V^T P^T over the block's 4 k-steps.
+        half8 pk[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int hh = 0; hh < 8; hh++)
+                pk[t][hh] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(st[t >> 1][8 * (t & 1) + hh], c2, -mc));
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                lsum = __builtin_amdgcn_fdot2(half2v{pk[t][2 * e], pk[t][2 * e + 1]}, ones, lsum, false);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DP / 32; dt++) {
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-#pragma unroll
-                for (int hh = 0; hh < 8; hh++) {
-                    float p = __builtin_amdgcn_exp2f(st[t >> 1][8 * (t & 1) + hh] - mn);
-                    ps += p;
-                    pk[t][hh] = (half_t)p;
+                half8 vop;
+                if (D < 32 && (grp & 1)) {
+                    vop = half8{};  // V^T rows D .. 31 of the padded tile
+                } else {
+                    const char* pv = st_base + vaddr[dt] + 16 * t * ROWB;
+                    const half4 lo = lds_read_tr(pv), hi = lds_read_tr(pv + 8 * ROWB);
+                    vop = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 }
-            }
-            lsum = lsum * alpha + ps;
-            m = mn;
-#pragma unroll
-            for (int dt = 0; dt < DP / 32; dt++) {
-                acc[dt] *= alpha;
-                const int d = dt * 32 + (lane & 31);
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    u32x2 lo = lds_v[buf][d * (BKEY / 4) + ((4 * t + g4) ^ (d & 15))];
-                    u32x2 hi = lds_v[buf][d * (BKEY / 4) + ((4 * t + 2 + g4) ^ (d & 15))];
-                    half8 vop = __builtin_bit_cast(half8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-                    acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pk[t], acc[dt], 0, 0, 0);
-                }
+                acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pk[t], acc[dt], 0, 0, 0);
             }
         }
-        if (j + BKEY < kend) sstore(buf ^ 1);
-        __syncthreads();
     }
 
     const float l = lsum + __shfl_xor(lsum, 32, 64);
     if (myq < a.S) {
         u16* o = a.O + (long)myq * a.q_row + (long)h * a.q_head;
-        const float inv = 1.0f / l;
 #pragma unroll
         for (int dt = 0; dt < DP / 32; dt++)
 #pragma unroll
             for (int rg = 0; rg < 4; rg++) {
                 const int d = dt * 32 + 8 * rg + 4 * g4;
                 if (d >= D) continue;
-                u32x2 w;
-                w[0] = (uint32_t)f2h(acc[dt][4 * rg] / l) | ((uint32_t)f2h(acc[dt][4 * rg + 1] / l) << 16);
-                w[1] = (uint32_t)f2h(acc[dt][4 * rg + 2] / l) | ((uint32_t)f2h(acc[dt][4 * rg + 3] / l) << 16);
-                *reinterpret_cast<u32x2*>(o + d) = w;
+                uint32_t w0 = (uint32_t)f2h(acc[dt][4 * rg] / l) | ((uint32_t)f2h(acc[dt][4 * rg + 1] / l) << 16);
+                uint32_t w1 = (uint32_t)f2h(acc[dt][4 * rg + 2] / l) | ((uint32_t)f2h(acc[dt][4 * rg + 3] / l) << 16);
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<u32x2_t*>(o + d) = u32x2_t{w0, w1};
             }
-        (void)inv;
     }
 }
 
