@@ -27,6 +27,7 @@ struct DecArgs {
     u16* O;
     float* part;  // [B][G][NCH][QPG][2 + D]: m, l, acc
     int B, H, G, NP, P, MP, NCH;
+    int pshift;  // log2(P) (P is a power of two)
     float c2;  // scale * log2(e)
 };
 
@@ -205,6 +206,302 @@ __global__ __launch_bounds__(64) void decode_combine(DecArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core path (D = 64 or 128, P a multiple of 16). A workgroup owns
+// (b, kv head g, chunk of DEC_CHUNK pages); each wavefront walks 16-token
+// tiles of the chunk (tiles w, w + 4, ...), double-buffering each tile's K
+// and V rows (16 x 2D bytes each) into its own LDS stage with direct
+// buffer->LDS loads. Per tile:
+//   S^T = K Q^T      v_mfma_f32_16x16x32_f16, A = K rows (token l%16), B =
+//                    the QPG query heads (columns >= QPG are zero); lane l
+//                    then holds tokens 4(l/16)+r of head l%16
+//   O^T += V^T P^T   v_mfma_f32_16x16x16_f16 per 16 d; P^T is the S^T
+//                    accumulator layout, V^T comes from transposed LDS reads.
+// p stays f32 as in the .tl: it enters the MFMA as two f16 terms (hi + lo),
+// which carries 22 bits of it. Softmax runs in the log2 domain on scaled
+// scores with the running maximum moved lazily (by > 2^8 only). Tiles run to
+// the end of the sequence's last page (masked), as the .tl's per-page loop
+// does. A chunk's state merges across its 4 wavefronts in LDS; a sequence of
+// one chunk writes O directly, longer ones leave per-chunk states for
+// decode_merge.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_t;
+constexpr int TT = 16;  // tokens per tile
+
+TSL_DEV i32x4 buf_rsrc(const void* p, uint32_t bytes) {
+    const uint64_t x = reinterpret_cast<uint64_t>(p);
+    return i32x4{(int)(uint32_t)x, (int)(uint32_t)((x >> 32) & 0xffff), (int)bytes, 0x00020000};
+}
+
+// 16-byte-chunk XOR swizzles of a tile row (2D bytes). K: the 16 lanes of a
+// 16-byte read hit 16 rows at one logical chunk. V: the 32 lanes of an 8-byte
+// transposed read hit 8 rows at one 32-byte granule.
+template <int D>
+TSL_DEV int tswz_k(int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); }
+template <int D>
+TSL_DEV int tswz_v(int row) { return D == 128 ? 2 * (row & 7) : 2 * ((row >> 1) & 3); }
+
+template <int D, int QPG>
+__global__ __launch_bounds__(256, 2) void decode_tiles(DecArgs a) {
+    constexpr int ROWB = 2 * D, KCH = D / 8;
+    constexpr int TILE = TT * ROWB;    // bytes of K (or V) per tile
+    constexpr int NLD = TILE / 1024;   // 1 KB loads per matrix per tile
+    constexpr int RPL = 1024 / ROWB;   // rows per 1 KB load
+    constexpr int WSTAGE = 2 * TILE;   // K then V
+    constexpr float LAZY = 8.0f;
+    constexpr int WAIT_ONE = 0x0f70 | (2 * NLD);  // vmcnt(2 NLD): all but the newest tile's loads
+    static_assert(4 * QPG * (2 + D) * 4 <= 8 * WSTAGE, "merge area exceeds the staging LDS");
+    __shared__ __attribute__((aligned(16))) char lds[8 * WSTAGE];  // [wave][stage]
+    float(*red)[QPG][2 + D] = reinterpret_cast<float(*)[QPG][2 + D]>(lds);  // reused after the loop
+
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, col = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = blockIdx.x % a.NCH, bg = blockIdx.x / a.NCH;
+    const int g = bg % a.G, b = bg / a.G;
+    const int n = a.lens[b];
+    const int npages = n > 0 ? (n + a.P - 1) / a.P : 0;
+    const int nact = min((npages + DEC_CHUNK - 1) / DEC_CHUNK, a.NCH);
+    if (c >= nact) {
+        if (c == 0)  // lens 0: 0 / 0, as the .tl computes
+            for (int x = tid; x < QPG * D; x += 256) a.O[((long)b * a.H + g * QPG) * D + x] = f2h(0.0f / 0.0f);
+        return;
+    }
+    const int t_lo = c * DEC_CHUNK * a.P;
+    const int t_hi = c == a.NCH - 1 ? n : min(n, (c + 1) * DEC_CHUNK * a.P);
+    const int t_end = (t_hi + a.P - 1) / a.P * a.P;  // through the last page
+    const int ntile = (t_end - t_lo) / TT;
+    const int nt = wave < ntile ? (ntile - wave + 3) / 4 : 0;
+
+    // Q^T operand: lane l holds head l%16, d = 32 s + 8 (l/16) .. +8.
+    half8 qop[D / 32];
+#pragma unroll
+    for (int s = 0; s < D / 32; s++) {
+        u32x4 t = {0, 0, 0, 0};
+        if (col < QPG) t = *reinterpret_cast<const u32x4*>(a.Q + ((long)b * a.H + g * QPG + col) * D + 32 * s + 8 * grp);
+        qop[s] = __builtin_bit_cast(half8, t);
+    }
+
+    // Load offsets (bytes from the tile's first row): load q, lane i fills
+    // LDS chunk i % KCH of row q RPL + i / KCH with the logical chunk that
+    // the swizzle puts there.
+    const long tok_bytes = (long)a.G * D * 2;
+    uint32_t offk[NLD], offv[NLD];
+#pragma unroll
+    for (int q = 0; q < NLD; q++) {
+        const int row = q * RPL + lane / KCH, pc = lane % KCH;
+        offk[q] = (uint32_t)(row * tok_bytes + ((pc ^ tswz_k<D>(row)) * 16));
+        offv[q] = (uint32_t)(row * tok_bytes + ((pc ^ tswz_v<D>(row)) * 16));
+    }
+    const uint32_t lds_w = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds) + wave * 2 * WSTAGE;
+    const char* Kg = reinterpret_cast<const char*>(a.Kc) + (long)g * D * 2;
+    const char* Vg = reinterpret_cast<const char*>(a.Vc) + (long)g * D * 2;
+    // The chunk's table entries, one per lane (tiles past the table read page 0).
+    const int page_lo = c * DEC_CHUNK;
+    const int tab = lane < DEC_CHUNK && page_lo + lane < a.MP ? a.table[(long)b * a.MP + page_lo + lane] : 0;
+    auto issue = [&](int ti, int st) {
+        const int t0 = t_lo + ti * TT;
+        const int pi = t0 >> a.pshift;
+        const int page = pi < a.MP ? __builtin_amdgcn_readlane(tab, pi - page_lo) : 0;
+        const bool ok = page >= 0 && page < a.NP;  // outside the pool: zeros
+        const long shift = ((long)(ok ? page : 0) * a.P + (t0 & (a.P - 1))) * tok_bytes;
+        const uint32_t range = ok ? (uint32_t)(TT * tok_bytes) : 0u;
+        const i32x4 rk = buf_rsrc(Kg + shift, range), rv = buf_rsrc(Vg + shift, range);
+        const uint32_t sk = lds_w + st * WSTAGE, sv = sk + TILE;
+#pragma unroll
+        for (int q = 0; q < NLD; q++) {
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sk + q * 1024),
+                         "v"(offk[q]), "s"(rk));
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sv + q * 1024),
+                         "v"(offv[q]), "s"(rv));
+        }
+    };
+
+    // Operand addresses within a stage. K: row l%16, logical chunk 4 s + l/16.
+    // V^T by transposed reads: provider lane p of group G points at token row
+    // 4 G + p/4 and d = 16 dt + 4 (p%4) .. +3, so lane l receives d = 16 dt + l%16
+    // for tokens 4 G + 0..3.
+    uint32_t kaddr[D / 32], vaddr[D / 16];
+#pragma unroll
+    for (int s = 0; s < D / 32; s++) kaddr[s] = (uint32_t)(col * ROWB + (((4 * s + grp) ^ tswz_k<D>(col)) * 16));
+    const int vrow = 4 * grp + (col >> 2);
+#pragma unroll
+    for (int dt = 0; dt < D / 16; dt++) {
+        const int lc = 2 * dt + ((col & 3) >> 1);
+        vaddr[dt] = (uint32_t)(TILE + vrow * ROWB + ((lc ^ tswz_v<D>(vrow)) * 16) + 8 * (col & 1));
+    }
+
+    float m = -1e30f, lsum = 0.0f;  // running max of the scaled scores; this lane's share of l
+    float4v acc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; dt++) acc[dt] = float4v{};
+
+    // Q and the table entries have arrived before the first tile's loads are
+    // issued (the loop waits on those loads by count).
+#pragma unroll
+    for (int s = 0; s < D / 32; s++) asm volatile("" ::"v"(qop[s]));
+    asm volatile("" ::"v"(tab));
+    if (nt > 0) issue(wave, 0);
+    for (int i = 0; i < nt; i++) {
+        if (i + 1 < nt) {
+            issue(wave + 4 * (i + 1), (i + 1) & 1);
+            __builtin_amdgcn_s_waitcnt(WAIT_ONE);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0f70);
+        }
+        const char* sb = lds + (wave * 2 + (i & 1)) * WSTAGE;
+        float4v st = float4v{};
+#pragma unroll
+        for (int s = 0; s < D / 32; s++) {
+            const half8 kop = *reinterpret_cast<const half8*>(sb + kaddr[s]);
+            st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[s], st, 0, 0, 0);
+        }
+        const int t0 = t_lo + (wave + 4 * i) * TT + 4 * grp;  // token of register 0
+        float x[4], mb = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            x[r] = t0 + r < n ? st[r] * a.c2 : -INFINITY;
+            mb = fmaxf(mb, x[r]);
+        }
+        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        if (__builtin_amdgcn_ballot_w64(mb > m + LAZY) != 0) {
+            const float mn = fmaxf(m, mb);
+            const float alpha = __builtin_amdgcn_exp2f(m - mn);
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++) acc[dt] *= alpha;
+            m = mn;
+        }
+        half4 phi, plo;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float p = __builtin_amdgcn_exp2f(x[r] - m);
+            lsum += p;
+            phi[r] = (half_t)p;
+            plo[r] = (half_t)(p - (float)phi[r]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 16; dt++) {
+            const fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (__attribute__((address_space(3))) fp16x4_t*)(sb + vaddr[dt]));
+            const half4 vop = __builtin_bit_cast(half4, v);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, phi, acc[dt], 0, 0, 0);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, plo, acc[dt], 0, 0, 0);
+        }
+    }
+
+    // Merge the wavefronts: lane l holds head l%16, d = 16 dt + 4 (l/16) + r.
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    __syncthreads();  // every wave is done with its stages
+    if (col < QPG) {
+        if (grp == 0) {
+            red[wave][col][0] = m;
+            red[wave][col][1] = lsum;
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 16; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[wave][col][2 + 16 * dt + 4 * grp + r] = acc[dt][r];
+    }
+    __syncthreads();
+    float* part = a.part + (((long)b * a.G + g) * a.NCH) * QPG * (2 + D);
+    for (int x = tid; x < QPG * D; x += 256) {
+        const int i = x / D, d = x % D;
+        float M = red[0][i][0];
+        for (int w = 1; w < 4; w++) M = fmaxf(M, red[w][i][0]);
+        float L = 0.0f, A = 0.0f;
+        for (int w = 0; w < 4; w++) {
+            const float f = __builtin_amdgcn_exp2f(red[w][i][0] - M);
+            L += red[w][i][1] * f;
+            A += red[w][i][2 + d] * f;
+        }
+        if (nact == 1) {
+            a.O[((long)b * a.H + g * QPG + i) * D + d] = f2h(A / L);
+        } else {
+            float* pe = part + ((long)c * QPG + i) * (2 + D);
+            if (d == 0) {
+                pe[0] = M;
+                pe[1] = L;
+            }
+            pe[2 + d] = A;
+        }
+    }
+}
+
+// Merges the chunk states of (b, g) in chunk order: one workgroup per (b, g).
+// All partial states are fetched at once into LDS (one memory latency), then
+// each thread merges one (head, d).
+template <int D, int QPG>
+__global__ __launch_bounds__(256) void decode_merge(DecArgs a) {
+    constexpr int ST = QPG * (2 + D);  // floats per chunk state
+    extern __shared__ float sm[];      // [nact][QPG][2 + D]
+    const int bg = blockIdx.x, b = bg / a.G, g = bg % a.G;
+    const int n = a.lens[b];
+    const int npages = n > 0 ? (n + a.P - 1) / a.P : 0;
+    const int nact = min((npages + DEC_CHUNK - 1) / DEC_CHUNK, a.NCH);
+    if (nact <= 1) return;  // written by the chunk kernel
+    const float4v* src = reinterpret_cast<const float4v*>(a.part + (long)bg * a.NCH * ST);
+    float4v* dst = reinterpret_cast<float4v*>(sm);
+    const int nv = nact * ST / 4;
+    for (int x0 = 0; x0 < nv; x0 += 256 * 8) {
+        float4v v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int x = x0 + u * 256 + (int)threadIdx.x;
+            if (x < nv) v[u] = src[x];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int x = x0 + u * 256 + (int)threadIdx.x;
+            if (x < nv) dst[x] = v[u];
+        }
+    }
+    __syncthreads();
+    for (int x = threadIdx.x; x < QPG * D; x += 256) {
+        const int i = x / D, d = x % D;
+        const float* pe = sm + i * (2 + D);
+        float M = pe[0];
+        for (int cc = 1; cc < nact; cc++) M = fmaxf(M, pe[cc * ST]);
+        float L = 0.0f, A = 0.0f;
+        for (int cc = 0; cc < nact; cc++) {
+            const float f = __builtin_amdgcn_exp2f(pe[cc * ST] - M);
+            L += pe[cc * ST + 1] * f;
+            A += pe[cc * ST + 2 + d] * f;
+        }
+        a.O[((long)b * a.H + g * QPG + i) * D + d] = f2h(A / L);
+    }
+}
+
+template <int D, int QPG>
+int run_decode_tiles(DecArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((decode_tiles<D, QPG>), dim3(a.B * a.G * a.NCH), dim3(256), 0, s, a);
+    int r = TSL_LAUNCHED("decode_attention");
+    if (r || a.NCH == 1) return r;
+    const size_t lds = (size_t)a.NCH * QPG * (2 + D) * sizeof(float);
+    if (lds > 65536) {  // too many states for one workgroup's LDS: the serial merge
+        hipLaunchKernelGGL((decode_combine<D, QPG>), dim3(a.B * a.H), dim3(64), 0, s, a);
+        return TSL_LAUNCHED("decode_attention combine");
+    }
+    hipLaunchKernelGGL((decode_merge<D, QPG>), dim3(a.B * a.G), dim3(256), lds, s, a);
+    return TSL_LAUNCHED("decode_attention merge");
+}
+
+template <int D>
+int run_tiles_d(DecArgs& a, int qpg, hipStream_t s) {
+    switch (qpg) {
+        case 1: return run_decode_tiles<D, 1>(a, s);
+        case 2: return run_decode_tiles<D, 2>(a, s);
+        case 4: return run_decode_tiles<D, 4>(a, s);
+        case 8: return run_decode_tiles<D, 8>(a, s);
+        case 16: return run_decode_tiles<D, 16>(a, s);
+    }
+    return tsl_fail(-2, "decode_attention: H / G must be 1, 2, 4, 8 or 16");
+}
+
+bool tiles_path(int64_t D, int64_t P) { return (D == 64 || D == 128) && P % TT == 0; }
+
 template <int D, int QPG>
 int run_decode(DecArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((decode_partial<D, QPG>), dim3(a.B * a.G * a.NCH), dim3(256), 0, s, a);
@@ -241,7 +538,7 @@ int prepare_decode(TslKernel& k) {
     if (qpg != 1 && qpg != 2 && qpg != 4 && qpg != 8 && qpg != 16)
         return tsl_fail(-2, k.name + ": H / G must be 1, 2, 4, 8 or 16");
     int nch = nchunks(k);
-    if (nch > 1) {
+    if (nch > 1) {  // [B][G][NCH][QPG][2 + D] per-chunk states
         size_t bytes = (size_t)k.dim("B") * G * nch * qpg * (2 + D) * sizeof(float);
         if (tsl_hip_check(hipMalloc(&k.scratch, bytes), "decode_attention scratch")) return -1;
         k.scratch_bytes = bytes;
@@ -263,11 +560,13 @@ static int launch_decode_common(TslKernel& k, const uint64_t* args, hipStream_t 
     a.G = gqa ? k.dim("G") : a.H;
     a.NP = k.dim("NP");
     a.P = k.dim("P");
+    a.pshift = __builtin_ctz((unsigned)a.P);
     a.MP = k.dim("MP");
     a.NCH = nchunks(k);
     a.part = reinterpret_cast<float*>(k.scratch);
     if (a.B == 0) return 0;
     const int D = k.dim("D"), qpg = a.H / a.G;
+    if (tiles_path(D, a.P)) return D == 128 ? run_tiles_d<128>(a, qpg, s) : run_tiles_d<64>(a, qpg, s);
     switch (D) {
         case 16: return run_decode_d<16>(a, qpg, s);
         case 32: return run_decode_d<32>(a, qpg, s);

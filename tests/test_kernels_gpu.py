@@ -228,13 +228,36 @@ def _decode(q, kc, vc, table, lens, scale):
 @pytest.mark.parametrize("cfg", [dict(b=64, h=32, g=8, d=128, p=16),
                                  dict(b=8, h=32, g=4, d=64, p=16, lo=1, hi=700),
                                  dict(b=5, h=4, g=2, d=16, p=8, lo=0, hi=60),
-                                 dict(b=3, h=8, g=8, d=32, p=16, lo=1, hi=300)])
+                                 dict(b=3, h=8, g=8, d=32, p=16, lo=1, hi=300),
+                                 dict(b=6, h=16, g=1, d=128, p=64, lo=1, hi=3000),
+                                 dict(b=9, h=8, g=4, d=64, p=32, lo=0, hi=2100)])
 def test_decode_attention_vs_oracle(cfg):
     _say("decode", cfg)
     q, kc, vc, table, lens, scale = decode_case(1, **cfg)
     want = oracle.decode_attention(q, kc, vc, table, lens, scale, threads=8)
     got = _decode(q, kc, vc, table, lens, scale)
     parity("decode", got, want)
+
+
+def test_decode_attention_repeat_launches():
+    """Multi-chunk sequences merge through per-(b, g) arrival counts that the
+    kernel returns to zero: back-to-back launches on one handle agree bit for
+    bit, and with the oracle."""
+    _say("decode repeat")
+    q, kc, vc, table, lens, scale = decode_case(4, b=12, h=32, g=8, d=128, p=16, lo=300, hi=4096)
+    T.open()
+    kern = T.kernel("llm", "decode_attention", [list(q.shape), list(kc.shape), list(vc.shape), list(table.shape),
+                                                 list(lens.shape), list(q.shape)])
+    bufs = [T.tensor(x) for x in (q, kc, vc, table, lens)] + [T.alloc(q.nbytes), T.F32(scale)]
+    outs = []
+    for _ in range(3):
+        T.launch(kern, bufs)
+        outs.append(T.read_array(bufs[5], np.float16, q.shape))
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.view(np.uint16), outs[0].view(np.uint16))
+    parity("decode repeat", outs[0], oracle.decode_attention(q, kc, vc, table, lens, scale, threads=8))
+    for x in bufs[:6]:
+        T.free(x)
 
 
 def test_decode_attention_indexing_properties():
