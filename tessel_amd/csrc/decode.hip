@@ -207,11 +207,11 @@ __global__ __launch_bounds__(64) void decode_combine(DecArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Matrix-core path (D = 64 or 128, P a multiple of 16). A workgroup owns
-// (b, kv head g, chunk of DEC_CHUNK pages); each wavefront walks 16-token
-// tiles of the chunk (tiles w, w + 4, ...), double-buffering each tile's K
-// and V rows (16 x 2D bytes each) into its own LDS stage with direct
-// buffer->LDS loads. Per tile:
+// Matrix-core path (D = 64 or 128, P a multiple of 16). A single-wavefront
+// workgroup owns (b, kv head g, chunk of DEC_CHUNK pages) and walks its
+// 16-token tiles through a DEC_STAGES-deep ring of LDS stages, each filled by
+// direct buffer->LDS loads (K rows then V rows, 16 x 2D bytes each), so that
+// DEC_STAGES - 1 tiles are in flight while one is computed. Per tile:
 //   S^T = K Q^T      v_mfma_f32_16x16x32_f16, A = K rows (token l%16), B =
 //                    the QPG query heads (columns >= QPG are zero); lane l
 //                    then holds tokens 4(l/16)+r of head l%16
@@ -221,13 +221,13 @@ __global__ __launch_bounds__(64) void decode_combine(DecArgs a) {
 // which carries 22 bits of it. Softmax runs in the log2 domain on scaled
 // scores with the running maximum moved lazily (by > 2^8 only). Tiles run to
 // the end of the sequence's last page (masked), as the .tl's per-page loop
-// does. A chunk's state merges across its 4 wavefronts in LDS; a sequence of
-// one chunk writes O directly, longer ones leave per-chunk states for
-// decode_merge.
+// does. A sequence of one chunk writes O directly; longer ones leave one
+// state per chunk for decode_merge.
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_t;
 constexpr int TT = 16;  // tokens per tile
+constexpr int DEC_STAGES = 3;  // LDS stages per wavefront: 2 tiles in flight
 
 TSL_DEV i32x4 buf_rsrc(const void* p, uint32_t bytes) {
     const uint64_t x = reinterpret_cast<uint64_t>(p);
@@ -242,36 +242,47 @@ TSL_DEV int tswz_k(int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); }
 template <int D>
 TSL_DEV int tswz_v(int row) { return D == 128 ? 2 * (row & 7) : 2 * ((row >> 1) & 3); }
 
-template <int D, int QPG>
-__global__ __launch_bounds__(256, 2) void decode_tiles(DecArgs a) {
-    constexpr int ROWB = 2 * D, KCH = D / 8;
-    constexpr int TILE = TT * ROWB;    // bytes of K (or V) per tile
-    constexpr int NLD = TILE / 1024;   // 1 KB loads per matrix per tile
-    constexpr int RPL = 1024 / ROWB;   // rows per 1 KB load
-    constexpr int WSTAGE = 2 * TILE;   // K then V
-    constexpr float LAZY = 8.0f;
-    constexpr int WAIT_ONE = 0x0f70 | (2 * NLD);  // vmcnt(2 NLD): all but the newest tile's loads
-    static_assert(4 * QPG * (2 + D) * 4 <= 8 * WSTAGE, "merge area exceeds the staging LDS");
-    __shared__ __attribute__((aligned(16))) char lds[8 * WSTAGE];  // [wave][stage]
-    float(*red)[QPG][2 + D] = reinterpret_cast<float(*)[QPG][2 + D]>(lds);  // reused after the loop
+// s_waitcnt immediate for vmcnt(n) alone (6-bit vmcnt: bits 3:0 and 15:14).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0f70; }
 
-    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, col = lane & 15;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int c = blockIdx.x % a.NCH, bg = blockIdx.x / a.NCH;
-    const int g = bg % a.G, b = bg / a.G;
+// Waits until at most `tiles` tiles (2 NLD loads each) are still loading.
+template <int NLD>
+TSL_DEV void wait_tiles(int tiles) {
+    switch (tiles) {  // s_waitcnt takes an immediate
+        case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NLD)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * NLD)); break;
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6 * NLD)); break;
+    }
+}
+
+template <int D, int QPG>
+__global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
+    constexpr int ROWB = 2 * D, KCH = D / 8;
+    constexpr int TILE = TT * ROWB;   // bytes of K (or V) per tile
+    constexpr int NLD = TILE / 1024;  // 1 KB loads per matrix per tile
+    constexpr int RPL = 1024 / ROWB;  // rows per 1 KB load
+    constexpr int WSTAGE = 2 * TILE;  // K then V
+    constexpr float LAZY = 8.0f;
+    static_assert(DEC_STAGES >= 2 && DEC_STAGES <= 4, "wait_tiles covers up to 3 tiles in flight");
+    __shared__ __attribute__((aligned(16))) char lds[DEC_STAGES * WSTAGE];
+
+    const int lane = threadIdx.x, grp = lane >> 4, col = lane & 15;
+    // The kv heads of one (b, chunk) are adjacent in launch order, so the
+    // pages' token rows (all G heads' 2D-byte slices) are read at one time.
+    const int g = blockIdx.x % a.G, c = (blockIdx.x / a.G) % a.NCH, b = blockIdx.x / (a.G * a.NCH);
     const int n = a.lens[b];
     const int npages = n > 0 ? (n + a.P - 1) / a.P : 0;
     const int nact = min((npages + DEC_CHUNK - 1) / DEC_CHUNK, a.NCH);
     if (c >= nact) {
         if (c == 0)  // lens 0: 0 / 0, as the .tl computes
-            for (int x = tid; x < QPG * D; x += 256) a.O[((long)b * a.H + g * QPG) * D + x] = f2h(0.0f / 0.0f);
+            for (int x = lane; x < QPG * D; x += 64) a.O[((long)b * a.H + g * QPG) * D + x] = f2h(0.0f / 0.0f);
         return;
     }
     const int t_lo = c * DEC_CHUNK * a.P;
     const int t_hi = c == a.NCH - 1 ? n : min(n, (c + 1) * DEC_CHUNK * a.P);
     const int t_end = (t_hi + a.P - 1) / a.P * a.P;  // through the last page
-    const int ntile = (t_end - t_lo) / TT;
-    const int nt = wave < ntile ? (ntile - wave + 3) / 4 : 0;
+    const int nt = (t_end - t_lo) / TT;
 
     // Q^T operand: lane l holds head l%16, d = 32 s + 8 (l/16) .. +8.
     half8 qop[D / 32];
@@ -281,6 +292,9 @@ __global__ __launch_bounds__(256, 2) void decode_tiles(DecArgs a) {
         if (col < QPG) t = *reinterpret_cast<const u32x4*>(a.Q + ((long)b * a.H + g * QPG + col) * D + 32 * s + 8 * grp);
         qop[s] = __builtin_bit_cast(half8, t);
     }
+    // The chunk's table entries, one per lane (tiles past the table read page 0).
+    const int page_lo = c * DEC_CHUNK;
+    const int tab = lane < DEC_CHUNK && page_lo + lane < a.MP ? a.table[(long)b * a.MP + page_lo + lane] : 0;
 
     // Load offsets (bytes from the tile's first row): load q, lane i fills
     // LDS chunk i % KCH of row q RPL + i / KCH with the logical chunk that
@@ -293,12 +307,9 @@ __global__ __launch_bounds__(256, 2) void decode_tiles(DecArgs a) {
         offk[q] = (uint32_t)(row * tok_bytes + ((pc ^ tswz_k<D>(row)) * 16));
         offv[q] = (uint32_t)(row * tok_bytes + ((pc ^ tswz_v<D>(row)) * 16));
     }
-    const uint32_t lds_w = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds) + wave * 2 * WSTAGE;
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
     const char* Kg = reinterpret_cast<const char*>(a.Kc) + (long)g * D * 2;
     const char* Vg = reinterpret_cast<const char*>(a.Vc) + (long)g * D * 2;
-    // The chunk's table entries, one per lane (tiles past the table read page 0).
-    const int page_lo = c * DEC_CHUNK;
-    const int tab = lane < DEC_CHUNK && page_lo + lane < a.MP ? a.table[(long)b * a.MP + page_lo + lane] : 0;
     auto issue = [&](int ti, int st) {
         const int t0 = t_lo + ti * TT;
         const int pi = t0 >> a.pshift;
@@ -307,7 +318,7 @@ __global__ __launch_bounds__(256, 2) void decode_tiles(DecArgs a) {
         const long shift = ((long)(ok ? page : 0) * a.P + (t0 & (a.P - 1))) * tok_bytes;
         const uint32_t range = ok ? (uint32_t)(TT * tok_bytes) : 0u;
         const i32x4 rk = buf_rsrc(Kg + shift, range), rv = buf_rsrc(Vg + shift, range);
-        const uint32_t sk = lds_w + st * WSTAGE, sv = sk + TILE;
+        const uint32_t sk = lds0 + st * WSTAGE, sv = sk + TILE;
 #pragma unroll
         for (int q = 0; q < NLD; q++) {
             asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sk + q * 1024),
@@ -336,31 +347,33 @@ __global__ __launch_bounds__(256, 2) void decode_tiles(DecArgs a) {
 #pragma unroll
     for (int dt = 0; dt < D / 16; dt++) acc[dt] = float4v{};
 
-    // Q and the table entries have arrived before the first tile's loads are
-    // issued (the loop waits on those loads by count).
+    // Q and the table entries have arrived before the tile loads are issued
+    // (the loop waits on those loads by count).
 #pragma unroll
     for (int s = 0; s < D / 32; s++) asm volatile("" ::"v"(qop[s]));
     asm volatile("" ::"v"(tab));
-    if (nt > 0) issue(wave, 0);
+    const int pre = min(nt, DEC_STAGES - 1);
+    for (int i = 0; i < pre; i++) issue(i, i);
+    int st = 0;
     for (int i = 0; i < nt; i++) {
-        if (i + 1 < nt) {
-            issue(wave + 4 * (i + 1), (i + 1) & 1);
-            __builtin_amdgcn_s_waitcnt(WAIT_ONE);
-        } else {
-            __builtin_amdgcn_s_waitcnt(0x0f70);
+        if (i + DEC_STAGES - 1 < nt) {
+            int sn = st + DEC_STAGES - 1;
+            issue(i + DEC_STAGES - 1, sn >= DEC_STAGES ? sn - DEC_STAGES : sn);
         }
-        const char* sb = lds + (wave * 2 + (i & 1)) * WSTAGE;
-        float4v st = float4v{};
+        wait_tiles<NLD>(min(nt - 1 - i, DEC_STAGES - 1));  // tile i has landed
+        const char* sb = lds + st * WSTAGE;
+        st = st + 1 == DEC_STAGES ? 0 : st + 1;
+        float4v sc = float4v{};
 #pragma unroll
         for (int s = 0; s < D / 32; s++) {
             const half8 kop = *reinterpret_cast<const half8*>(sb + kaddr[s]);
-            st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[s], st, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[s], sc, 0, 0, 0);
         }
-        const int t0 = t_lo + (wave + 4 * i) * TT + 4 * grp;  // token of register 0
+        const int t0 = t_lo + i * TT + 4 * grp;  // token of register 0
         float x[4], mb = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            x[r] = t0 + r < n ? st[r] * a.c2 : -INFINITY;
+            x[r] = t0 + r < n ? sc[r] * a.c2 : -INFINITY;
             mb = fmaxf(mb, x[r]);
         }
         mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
@@ -391,42 +404,27 @@ __global__ __launch_bounds__(256, 2) void decode_tiles(DecArgs a) {
         }
     }
 
-    // Merge the wavefronts: lane l holds head l%16, d = 16 dt + 4 (l/16) + r.
+    // Lane l holds head l%16, d = 16 dt + 4 (l/16) + r.
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
-    __syncthreads();  // every wave is done with its stages
-    if (col < QPG) {
+    if (col >= QPG) return;
+    if (nact == 1) {
+        u16* o = a.O + ((long)b * a.H + g * QPG + col) * D + 4 * grp;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; dt++) {
+            const uint32_t w0 = (uint32_t)f2h(acc[dt][0] / lsum) | ((uint32_t)f2h(acc[dt][1] / lsum) << 16);
+            const uint32_t w1 = (uint32_t)f2h(acc[dt][2] / lsum) | ((uint32_t)f2h(acc[dt][3] / lsum) << 16);
+            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<u32x2_t*>(o + 16 * dt) = u32x2_t{w0, w1};
+        }
+    } else {
+        float* pe = a.part + ((((long)b * a.G + g) * a.NCH + c) * QPG + col) * (2 + D);
         if (grp == 0) {
-            red[wave][col][0] = m;
-            red[wave][col][1] = lsum;
+            pe[0] = m;
+            pe[1] = lsum;
         }
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) red[wave][col][2 + 16 * dt + 4 * grp + r] = acc[dt][r];
-    }
-    __syncthreads();
-    float* part = a.part + (((long)b * a.G + g) * a.NCH) * QPG * (2 + D);
-    for (int x = tid; x < QPG * D; x += 256) {
-        const int i = x / D, d = x % D;
-        float M = red[0][i][0];
-        for (int w = 1; w < 4; w++) M = fmaxf(M, red[w][i][0]);
-        float L = 0.0f, A = 0.0f;
-        for (int w = 0; w < 4; w++) {
-            const float f = __builtin_amdgcn_exp2f(red[w][i][0] - M);
-            L += red[w][i][1] * f;
-            A += red[w][i][2 + d] * f;
-        }
-        if (nact == 1) {
-            a.O[((long)b * a.H + g * QPG + i) * D + d] = f2h(A / L);
-        } else {
-            float* pe = part + ((long)c * QPG + i) * (2 + D);
-            if (d == 0) {
-                pe[0] = M;
-                pe[1] = L;
-            }
-            pe[2 + d] = A;
-        }
+        for (int dt = 0; dt < D / 16; dt++) *reinterpret_cast<float4v*>(pe + 2 + 16 * dt + 4 * grp) = acc[dt];
     }
 }
 
@@ -476,7 +474,7 @@ __global__ __launch_bounds__(256) void decode_merge(DecArgs a) {
 
 template <int D, int QPG>
 int run_decode_tiles(DecArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((decode_tiles<D, QPG>), dim3(a.B * a.G * a.NCH), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((decode_tiles<D, QPG>), dim3(a.B * a.G * a.NCH), dim3(64), 0, s, a);
     int r = TSL_LAUNCHED("decode_attention");
     if (r || a.NCH == 1) return r;
     const size_t lds = (size_t)a.NCH * QPG * (2 + D) * sizeof(float);
