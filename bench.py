@@ -209,13 +209,13 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--llm", action="store_true", help="also run the TinyLlama decode case (config 5)")
     ap.add_argument("--only", default="", help="comma list of cases: gemm1024,gemm2048,fa512..fa4096,decode,"
-                    "rmsnorm,softmax,llm; 'none' for the headline GEMM alone")
+                    "rmsnorm,softmax,llm,copy (counter calibration); 'none' for the headline GEMM alone")
     ap.add_argument("--profile", action="store_true",
                     help="few launches, no clock warm-up: for rocprofv3 counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the kernels run on one MI355X; sharding is described in DESIGN.md)", file=sys.stderr)
+              "(every kernel here runs on one MI355X; the measured value is one GPU's throughput)", file=sys.stderr)
         sys.exit(2)
 
     import tessel_amd as T
@@ -238,8 +238,8 @@ def main():
     ms = g.run(args.steps)
     wall = time.perf_counter() - wall0
     value = flops / (ms * 1e-3) / 1e12
-    kern_ms = g.median(50)  # the kernel's average launch duration, for the roofline
-    achieved = flops / (kern_ms * 1e-3) / 1e12
+    kern_ms = ms  # one launch per step: the kernel's average duration over the timed region
+    achieved = value
     traffic = load_traffic("matmul_4096")
     line = {
         "metric": "fp16 GEMM/attn TFLOP/s, paged-decode HBM GB/s, % of MI355X roofline",
@@ -250,7 +250,7 @@ def main():
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_MFMA_F16, 4), "traffic": traffic,
-                     "kernel": "gemm_f16<256,256,64,2,2> (matmul)", "kernel_ms": round(kern_ms, 5),
+                     "kernel": "gemm_big<false, 0, 256, 256, 2, 4> (matmul)", "kernel_ms": round(kern_ms, 5),
                      "algorithmic_per_launch": "2MNK = 137.44 GFLOP"},
         "device": {"name": T.device_name(), "cus": cus, "mhz": mhz},
     }
@@ -284,6 +284,14 @@ def main():
                           "gbps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4), "bytes": nb,
                           "context_tokens": toks, "tflops": round(fl / m / 1e9, 3),
                           "traffic": load_traffic("decode_attention")})
+        if "copy" in only:  # counter calibration (rocprofv3 passes), not a bench line
+            n = 32 << 20
+            bufs = [T.alloc(4 * n), T.alloc(4 * n), T.alloc(4 * n)]
+            t = Timed(T, T.kernel("basic", "add", [[n]] * 3), bufs)
+            t.warm()
+            m = t.median(20)
+            cases.append({"case": "add f32 32Mi (reads 256 MiB, writes 128 MiB)", "ms": round(m, 5),
+                          "gbps": round(12.0 * n / m / 1e6, 1)})
         for kind in ("rmsnorm", "softmax"):
             if not want(kind):
                 continue
