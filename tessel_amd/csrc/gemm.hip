@@ -482,6 +482,120 @@ __global__ __launch_bounds__(256) void matmul_f32_kernel(const float* __restrict
         }
 }
 
+// ---------------------------------------------------------------- the skinny path
+// Y = X W^T with few rows (M <= 64: the engine's decode steps) is a stream of
+// W, N x K x 2 bytes, so it is laid out for bandwidth: a workgroup of 8
+// wavefronts owns 16 rows of W and the wavefronts take interleaved 64-wide
+// steps of K, so a workgroup reads neighbouring 128-byte segments of the same
+// rows together. An MFMA operand load is 16 rows x 64 contiguous bytes (4
+// lanes a row), the two halves of a row's 128-byte segment in consecutive
+// loads, and
+//   Y^T (16 n x 16 m) += W (16 n x 32 k) X^T (32 k x 16 m)
+// runs on v_mfma_f32_16x16x32_f16, one 16-row tile of X per MT. The 8
+// partial tiles are summed in LDS in wavefront order (deterministic), then
+// the epilogue writes Y. Needs K % 64 == 0; rows past M or N read as zero and
+// their outputs are dropped.
+constexpr int SK_WAVES = 8;
+
+template <int EPI, int MT>
+__global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const u16* __restrict__ X, const u16* __restrict__ W,
+                                                               const u16* __restrict__ W2, void* C,
+                                                               const u16* __restrict__ bias, int M, int N, int K) {
+    constexpr bool DUAL = EPI == EPI_SWIGLU;
+    constexpr int NACC = DUAL ? 2 * MT : MT;
+    __shared__ float red[SK_WAVES][NACC][4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int row = lane & 15, g = lane >> 4;
+    const bool nok = n0 + row < N;
+    const u16* wp = W + (size_t)(nok ? n0 + row : 0) * K + 8 * g;
+    const u16* wp2 = DUAL ? W2 + (size_t)(nok ? n0 + row : 0) * K + 8 * g : nullptr;
+    const u16* xp[MT];
+    bool mok[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        mok[t] = 16 * t + row < M;
+        xp[t] = X + (size_t)(mok[t] ? 16 * t + row : 0) * K + 8 * g;
+    }
+    float4v acc[NACC];
+#pragma unroll
+    for (int i = 0; i < NACC; i++) acc[i] = float4v{};
+    const u32x4 z = {0, 0, 0, 0};
+    const int nst = K / 64;
+    constexpr int U = 2;  // steps in flight per wavefront
+    auto step = [&](const u32x4 (&w)[2], const u32x4 (&w2)[2], const u32x4 (&x)[MT][2]) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const half8 xo = __builtin_bit_cast(half8, x[t][i]);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, w[i]), xo, acc[t], 0, 0, 0);
+                if constexpr (DUAL)
+                    acc[MT + t] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, w2[i]), xo, acc[MT + t], 0, 0, 0);
+            }
+    };
+    auto load = [&](int kb, u32x4 (&w)[2], u32x4 (&w2)[2], u32x4 (&x)[MT][2]) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            w[i] = nok ? ldg16(wp + kb + 32 * i) : z;
+            if constexpr (DUAL) w2[i] = nok ? ldg16(wp2 + kb + 32 * i) : z;
+#pragma unroll
+            for (int t = 0; t < MT; t++) x[t][i] = mok[t] ? ldg16(xp[t] + kb + 32 * i) : z;
+        }
+    };
+    int st = wave;
+    for (; st + SK_WAVES * (U - 1) < nst; st += SK_WAVES * U) {
+        u32x4 w[U][2], w2[U][2], x[U][MT][2];
+#pragma unroll
+        for (int u = 0; u < U; u++) load(64 * (st + SK_WAVES * u), w[u], w2[u], x[u]);
+#pragma unroll
+        for (int u = 0; u < U; u++) step(w[u], w2[u], x[u]);
+    }
+    for (; st < nst; st += SK_WAVES) {  // the remaining steps, one at a time
+        u32x4 w[2], w2[2], x[MT][2];
+        load(64 * st, w, w2, x);
+        step(w, w2, x);
+    }
+#pragma unroll
+    for (int i = 0; i < NACC; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[wave][i][r][lane] = acc[i][r];
+    __syncthreads();
+    // Element (r, l) of tile t: output n = n0 + 4 (l/16) + r, m = 16 t + l%16.
+    for (int e = tid; e < MT * 256; e += 64 * SK_WAVES) {
+        const int t = e >> 8, r = (e >> 6) & 3, l = e & 63;
+        const int n = n0 + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
+        float v = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int w = 0; w < SK_WAVES; w++) {
+            v += red[w][t][r][l];
+            if constexpr (DUAL) u += red[w][MT + t][r][l];
+        }
+        if (m >= M || n >= N) continue;
+        const size_t o = (size_t)m * N + n;
+        if constexpr (EPI == EPI_F16) {
+            reinterpret_cast<u16*>(C)[o] = f2h(v);
+        } else if constexpr (EPI == EPI_F32) {
+            reinterpret_cast<float*>(C)[o] = v;
+        } else if constexpr (EPI == EPI_RESID) {
+            float* R = reinterpret_cast<float*>(C);
+            R[o] = R[o] + v;
+        } else if constexpr (EPI == EPI_BIAS) {
+            reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[n]));
+        } else {
+            reinterpret_cast<u16*>(C)[o] = f2h(v / (1.0f + expf(-v)) * u);
+        }
+    }
+}
+
+template <int EPI, int MT>
+void launch_skinny(const u16* X, const u16* W, const u16* W2, void* C, const u16* bias, int M, int N, int K,
+                   hipStream_t s) {
+    hipLaunchKernelGGL((gemm_skinny<EPI, MT>), dim3((N + 15) / 16), dim3(64 * SK_WAVES), 0, s, X, W, W2, C, bias, M, N,
+                       K);
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, bool BT, int EPI>
 int run_gemm(const u16* A, const u16* B, const u16* B2, void* C, const u16* bias, int M, int N, int K,
              hipStream_t s, const char* what) {
@@ -499,6 +613,17 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
                   hipStream_t s, const char* what) {
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     constexpr bool DUAL = EPI == EPI_SWIGLU;
+    if constexpr (BT) {
+        if (M > 0 && M <= 64 && N > 0 && K % 64 == 0) {  // a weight stream: the skinny path
+            switch ((M + 15) / 16) {
+                case 1: launch_skinny<EPI, 1>(A, B, B2, C, bias, M, N, K, s); break;
+                case 2: launch_skinny<EPI, 2>(A, B, B2, C, bias, M, N, K, s); break;
+                case 3: launch_skinny<EPI, 3>(A, B, B2, C, bias, M, N, K, s); break;
+                default: launch_skinny<EPI, 4>(A, B, B2, C, bias, M, N, K, s); break;
+            }
+            return TSL_LAUNCHED(what);
+        }
+    }
     if constexpr (!DUAL) {
         const bool aligned = (K % 8) == 0 && (BT || (N % 8) == 0) && (long)M * K < (1L << 30) &&
                              (long)N * K < (1L << 30);
