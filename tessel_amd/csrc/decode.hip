@@ -15,10 +15,12 @@
 // lens[b] == 0 gives 0/0 = NaN, as in the .tl.
 #include "common.h"
 
+#include <algorithm>
+
 namespace {
 
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr int DEC_CHUNK = 16;  // pages per workgroup
+constexpr int DEC_MAX_CHUNK = 16;  // pages per workgroup, at most (one table entry per lane)
 
 struct DecArgs {
     const u16* Q;
@@ -27,6 +29,7 @@ struct DecArgs {
     u16* O;
     float* part;  // [B][G][NCH][QPG][2 + D]: m, l, acc
     int B, H, G, NP, P, MP, NCH;
+    int CH;  // pages per chunk
     int pshift;  // log2(P) (P is a power of two)
     float c2;  // scale * log2(e)
 };
@@ -56,11 +59,16 @@ __global__ __launch_bounds__(256) void decode_partial(DecArgs a) {
     const int g = bg % a.G, b = bg / a.G;
     const int n = a.lens[b];
     const int npages = n > 0 ? (n + a.P - 1) / a.P : 0;
-    const int page_lo = c * DEC_CHUNK;
-    if (page_lo >= npages && !(a.NCH == 1)) return;  // nothing here (the combine skips this chunk)
+    const int page_lo = c * a.CH;
+    const int nact = min((npages + a.CH - 1) / a.CH, a.NCH);  // chunks holding tokens
+    if (c >= nact) {
+        if (c == 0)  // lens 0: 0 / 0, as the .tl computes
+            for (int x = threadIdx.x; x < QPG * D; x += 256) a.O[((long)b * a.H + g * QPG) * D + x] = f2h(0.0f / 0.0f);
+        return;
+    }
     // The last chunk also takes tokens past MP * P (their table reads give page 0).
     const int t_lo = page_lo * a.P;
-    const int t_hi = c == a.NCH - 1 ? n : min(n, (page_lo + DEC_CHUNK) * a.P);
+    const int t_hi = c == a.NCH - 1 ? n : min(n, (page_lo + a.CH) * a.P);
     const int dl = lane % LPT, tg = lane / LPT;
 
     // q of the QPG heads of group g, this lane's 8 d values, as f16 pairs.
@@ -170,7 +178,7 @@ __global__ __launch_bounds__(256) void decode_partial(DecArgs a) {
             L += red[w][i][1] * f;
             A += red[w][i][2 + d] * f;
         }
-        if (a.NCH == 1) {
+        if (nact == 1) {  // the only chunk: O directly
             a.O[((long)b * a.H + g * QPG + i) * D + d] = f2h(A / L);
         } else {
             float* pe = a.part + ((((long)b * a.G + g) * a.NCH + c) * QPG + i) * (2 + D);
@@ -184,13 +192,15 @@ __global__ __launch_bounds__(256) void decode_partial(DecArgs a) {
 }
 
 // Merges the chunks of (b, h) in chunk order: one wavefront per (b, h).
+// Sequences of at most one chunk were written by the chunk kernel.
 template <int D, int QPG>
 __global__ __launch_bounds__(64) void decode_combine(DecArgs a) {
     const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
     const int g = h / QPG, i = h % QPG;
     const int n = a.lens[b];
     const int npages = n > 0 ? (n + a.P - 1) / a.P : 0;
-    const int nch = min((npages + DEC_CHUNK - 1) / DEC_CHUNK, a.NCH);
+    const int nch = min((npages + a.CH - 1) / a.CH, a.NCH);
+    if (nch <= 1) return;  // written by the chunk kernel
     const float* base = a.part + (((long)b * a.G + g) * a.NCH * QPG + i) * (2 + D);
     const long cs = (long)QPG * (2 + D);
     float M = -INFINITY;
@@ -208,7 +218,7 @@ __global__ __launch_bounds__(64) void decode_combine(DecArgs a) {
 
 // ---------------------------------------------------------------------------
 // Matrix-core path (D = 64 or 128, P a multiple of 16). A single-wavefront
-// workgroup owns (b, kv head g, chunk of DEC_CHUNK pages) and walks its
+// workgroup owns (b, kv head g, chunk of CH pages) and walks its
 // 16-token tiles through a DEC_STAGES-deep ring of LDS stages, each filled by
 // direct buffer->LDS loads (K rows then V rows, 16 x 2D bytes each), so that
 // DEC_STAGES - 1 tiles are in flight while one is computed. Per tile:
@@ -273,14 +283,14 @@ __global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
     const int g = blockIdx.x % a.G, c = (blockIdx.x / a.G) % a.NCH, b = blockIdx.x / (a.G * a.NCH);
     const int n = a.lens[b];
     const int npages = n > 0 ? (n + a.P - 1) / a.P : 0;
-    const int nact = min((npages + DEC_CHUNK - 1) / DEC_CHUNK, a.NCH);
+    const int nact = min((npages + a.CH - 1) / a.CH, a.NCH);
     if (c >= nact) {
         if (c == 0)  // lens 0: 0 / 0, as the .tl computes
             for (int x = lane; x < QPG * D; x += 64) a.O[((long)b * a.H + g * QPG) * D + x] = f2h(0.0f / 0.0f);
         return;
     }
-    const int t_lo = c * DEC_CHUNK * a.P;
-    const int t_hi = c == a.NCH - 1 ? n : min(n, (c + 1) * DEC_CHUNK * a.P);
+    const int t_lo = c * a.CH * a.P;
+    const int t_hi = c == a.NCH - 1 ? n : min(n, (c + 1) * a.CH * a.P);
     const int t_end = (t_hi + a.P - 1) / a.P * a.P;  // through the last page
     const int nt = (t_end - t_lo) / TT;
 
@@ -293,8 +303,8 @@ __global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
         qop[s] = __builtin_bit_cast(half8, t);
     }
     // The chunk's table entries, one per lane (tiles past the table read page 0).
-    const int page_lo = c * DEC_CHUNK;
-    const int tab = lane < DEC_CHUNK && page_lo + lane < a.MP ? a.table[(long)b * a.MP + page_lo + lane] : 0;
+    const int page_lo = c * a.CH;
+    const int tab = lane < a.CH && page_lo + lane < a.MP ? a.table[(long)b * a.MP + page_lo + lane] : 0;
 
     // Load offsets (bytes from the tile's first row): load q, lane i fills
     // LDS chunk i % KCH of row q RPL + i / KCH with the logical chunk that
@@ -438,7 +448,7 @@ __global__ __launch_bounds__(256) void decode_merge(DecArgs a) {
     const int bg = blockIdx.x, b = bg / a.G, g = bg % a.G;
     const int n = a.lens[b];
     const int npages = n > 0 ? (n + a.P - 1) / a.P : 0;
-    const int nact = min((npages + DEC_CHUNK - 1) / DEC_CHUNK, a.NCH);
+    const int nact = min((npages + a.CH - 1) / a.CH, a.NCH);
     if (nact <= 1) return;  // written by the chunk kernel
     const float4v* src = reinterpret_cast<const float4v*>(a.part + (long)bg * a.NCH * ST);
     float4v* dst = reinterpret_cast<float4v*>(sm);
@@ -521,7 +531,21 @@ int run_decode_d(DecArgs& a, int qpg, hipStream_t s) {
     return tsl_fail(-2, "decode_attention: H / G must be 1, 2, 4, 8 or 16");
 }
 
-int nchunks(const TslKernel& k) { return (int)((k.dim("MP") + DEC_CHUNK - 1) / DEC_CHUNK); }
+// Pages per chunk: enough chunks for about 2048 workgroups over B x G at the
+// table's full length (short contexts get short chunks, so the cache is
+// still read by the whole chip), few enough that one (b, g)'s chunk states
+// fit the merge's 64 KB of LDS; between 2 and 16 pages.
+int chunk_pages(const TslKernel& k) {
+    const int64_t H = k.dim("H"), G = k.name == "paged_attention" ? H : k.dim("G");
+    const int64_t bg = std::max<int64_t>(1, k.dim("B") * G), mp = k.dim("MP");
+    const int64_t state = (H / std::max<int64_t>(1, G)) * (2 + k.dim("D")) * 4;  // bytes per chunk
+    const int64_t ch = std::max((mp * bg + 2047) / 2048, (mp * state + 65535) / 65536);
+    return (int)std::min<int64_t>(DEC_MAX_CHUNK, std::max<int64_t>(2, ch));
+}
+int nchunks(const TslKernel& k) {
+    const int ch = chunk_pages(k);
+    return (int)((k.dim("MP") + ch - 1) / ch);
+}
 
 }  // namespace
 
@@ -561,6 +585,7 @@ static int launch_decode_common(TslKernel& k, const uint64_t* args, hipStream_t 
     a.pshift = __builtin_ctz((unsigned)a.P);
     a.MP = k.dim("MP");
     a.NCH = nchunks(k);
+    a.CH = chunk_pages(k);
     a.part = reinterpret_cast<float*>(k.scratch);
     if (a.B == 0) return 0;
     const int D = k.dim("D"), qpg = a.H / a.G;
