@@ -14,6 +14,8 @@
 // dropped, which is the interpreter's rule (src/interp.rs:93-117, :296-313).
 #include "common.h"
 
+#include <algorithm>
+
 namespace {
 
 constexpr int NUM_XCD = 8;
@@ -497,19 +499,48 @@ __global__ __launch_bounds__(256) void matmul_f32_kernel(const float* __restrict
 // their outputs are dropped.
 constexpr int SK_WAVES = 8;
 
-template <int EPI, int MT>
+// The epilogue of one output (m, n): v = (X W^T)[m, n], u its SwiGLU partner.
+template <int EPI>
+TSL_DEV void sk_store(void* C, const u16* bias, int N, int m, int n, float v, float u) {
+    const size_t o = (size_t)m * N + n;
+    if constexpr (EPI == EPI_F16) {
+        reinterpret_cast<u16*>(C)[o] = f2h(v);
+    } else if constexpr (EPI == EPI_F32) {
+        reinterpret_cast<float*>(C)[o] = v;
+    } else if constexpr (EPI == EPI_RESID) {
+        float* R = reinterpret_cast<float*>(C);
+        R[o] = R[o] + v;
+    } else if constexpr (EPI == EPI_BIAS) {
+        reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[n]));
+    } else {
+        reinterpret_cast<u16*>(C)[o] = f2h(v / (1.0f + expf(-v)) * u);
+    }
+}
+
+// RT 16-row tiles of W per workgroup (one X load feeds all of them); with
+// SPLIT, workgroup (b, ks) covers the ks-th of gridDim.y slices of the K
+// steps and leaves its sums in part[ks][p][m][n] (p: gate, up) for
+// skinny_reduce.
+template <int EPI, int MT, int RT, bool SPLIT>
 __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const u16* __restrict__ X, const u16* __restrict__ W,
                                                                const u16* __restrict__ W2, void* C,
-                                                               const u16* __restrict__ bias, int M, int N, int K) {
+                                                               const u16* __restrict__ bias, int M, int N, int K,
+                                                               float* __restrict__ part) {
     constexpr bool DUAL = EPI == EPI_SWIGLU;
-    constexpr int NACC = DUAL ? 2 * MT : MT;
-    __shared__ float red[SK_WAVES][NACC][4][64];
+    constexpr int NW = DUAL ? 2 * RT : RT;  // W tiles per step (gate rows then up rows)
+    constexpr int NACC = NW * MT;
+    __shared__ float red[SK_WAVES][4][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16 * RT;
     const int row = lane & 15, g = lane >> 4;
-    const bool nok = n0 + row < N;
-    const u16* wp = W + (size_t)(nok ? n0 + row : 0) * K + 8 * g;
-    const u16* wp2 = DUAL ? W2 + (size_t)(nok ? n0 + row : 0) * K + 8 * g : nullptr;
+    const u16* wp[NW];
+    bool nok[NW];
+#pragma unroll
+    for (int r = 0; r < NW; r++) {
+        const int n = n0 + 16 * (r % RT) + row;
+        nok[r] = n < N;
+        wp[r] = (DUAL && r >= RT ? W2 : W) + (size_t)(nok[r] ? n : 0) * K + 8 * g;
+    }
     const u16* xp[MT];
     bool mok[MT];
 #pragma unroll
@@ -517,83 +548,135 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const u16* __restri
         mok[t] = 16 * t + row < M;
         xp[t] = X + (size_t)(mok[t] ? 16 * t + row : 0) * K + 8 * g;
     }
-    float4v acc[NACC];
+    float4v acc[NACC];  // [W tile][m tile]
 #pragma unroll
     for (int i = 0; i < NACC; i++) acc[i] = float4v{};
     const u32x4 z = {0, 0, 0, 0};
-    const int nst = K / 64;
+    const int nst = K / 64, S = SPLIT ? gridDim.y : 1, ks = SPLIT ? blockIdx.y : 0;
+    const int st_hi = (int)((long)(ks + 1) * nst / S);
     constexpr int U = 2;  // steps in flight per wavefront
-    auto step = [&](const u32x4 (&w)[2], const u32x4 (&w2)[2], const u32x4 (&x)[MT][2]) {
+    auto step = [&](const u32x4 (&w)[NW][2], const u32x4 (&x)[MT][2]) {
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int t = 0; t < MT; t++) {
-                const half8 xo = __builtin_bit_cast(half8, x[t][i]);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, w[i]), xo, acc[t], 0, 0, 0);
-                if constexpr (DUAL)
-                    acc[MT + t] =
-                        __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, w2[i]), xo, acc[MT + t], 0, 0, 0);
-            }
+            for (int r = 0; r < NW; r++)
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+                    acc[r * MT + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(half8, w[r][i]), __builtin_bit_cast(half8, x[t][i]), acc[r * MT + t], 0, 0,
+                        0);
     };
-    auto load = [&](int kb, u32x4 (&w)[2], u32x4 (&w2)[2], u32x4 (&x)[MT][2]) {
+    auto load = [&](int kb, u32x4 (&w)[NW][2], u32x4 (&x)[MT][2]) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            w[i] = nok ? ldg16(wp + kb + 32 * i) : z;
-            if constexpr (DUAL) w2[i] = nok ? ldg16(wp2 + kb + 32 * i) : z;
+#pragma unroll
+            for (int r = 0; r < NW; r++) w[r][i] = nok[r] ? ldg16(wp[r] + kb + 32 * i) : z;
 #pragma unroll
             for (int t = 0; t < MT; t++) x[t][i] = mok[t] ? ldg16(xp[t] + kb + 32 * i) : z;
         }
     };
-    int st = wave;
-    for (; st + SK_WAVES * (U - 1) < nst; st += SK_WAVES * U) {
-        u32x4 w[U][2], w2[U][2], x[U][MT][2];
+    int st = (int)((long)ks * nst / S) + wave;
+    for (; st + SK_WAVES * (U - 1) < st_hi; st += SK_WAVES * U) {
+        u32x4 w[U][NW][2], x[U][MT][2];
 #pragma unroll
-        for (int u = 0; u < U; u++) load(64 * (st + SK_WAVES * u), w[u], w2[u], x[u]);
+        for (int u = 0; u < U; u++) load(64 * (st + SK_WAVES * u), w[u], x[u]);
 #pragma unroll
-        for (int u = 0; u < U; u++) step(w[u], w2[u], x[u]);
+        for (int u = 0; u < U; u++) step(w[u], x[u]);
     }
-    for (; st < nst; st += SK_WAVES) {  // the remaining steps, one at a time
-        u32x4 w[2], w2[2], x[MT][2];
-        load(64 * st, w, w2, x);
-        step(w, w2, x);
+    for (; st < st_hi; st += SK_WAVES) {  // the remaining steps, one at a time
+        u32x4 w[NW][2], x[MT][2];
+        load(64 * st, w, x);
+        step(w, x);
     }
+    // Sum the 8 partial tiles, one accumulator at a time through LDS; thread
+    // tid < 256 keeps element tid (register tid/64 of lane tid%64) of each.
+    float sum[NACC];
 #pragma unroll
-    for (int i = 0; i < NACC; i++)
+    for (int i = 0; i < NACC; i++) {
+        if (i) __syncthreads();
 #pragma unroll
-        for (int r = 0; r < 4; r++) red[wave][i][r][lane] = acc[i][r];
-    __syncthreads();
-    // Element (r, l) of tile t: output n = n0 + 4 (l/16) + r, m = 16 t + l%16.
-    for (int e = tid; e < MT * 256; e += 64 * SK_WAVES) {
-        const int t = e >> 8, r = (e >> 6) & 3, l = e & 63;
-        const int n = n0 + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
-        float v = 0.0f, u = 0.0f;
+        for (int r = 0; r < 4; r++) red[wave][r][lane] = acc[i][r];
+        __syncthreads();
+        float v = 0.0f;
+        if (tid < 256)
 #pragma unroll
-        for (int w = 0; w < SK_WAVES; w++) {
-            v += red[w][t][r][l];
-            if constexpr (DUAL) u += red[w][MT + t][r][l];
+            for (int w = 0; w < SK_WAVES; w++) v += red[w][tid >> 6][tid & 63];
+        sum[i] = v;
+    }
+    if (tid >= 256) return;
+    // Element (r, l) of tile (rt, t): output n = n0 + 16 rt + 4 (l/16) + r, m = 16 t + l%16.
+    const int r = tid >> 6, l = tid & 63;
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int n = n0 + 16 * rt + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
+            if (m >= M || n >= N) continue;
+            const float v = sum[rt * MT + t], u = DUAL ? sum[(RT + rt) * MT + t] : 0.0f;
+            if constexpr (SPLIT) {
+                constexpr int NP = DUAL ? 2 : 1;
+                float* pp = part + (size_t)ks * NP * M * N + (size_t)m * N + n;
+                pp[0] = v;
+                if constexpr (DUAL) pp[(size_t)M * N] = u;
+            } else {
+                sk_store<EPI>(C, bias, N, m, n, v, u);
+            }
         }
-        if (m >= M || n >= N) continue;
-        const size_t o = (size_t)m * N + n;
-        if constexpr (EPI == EPI_F16) {
-            reinterpret_cast<u16*>(C)[o] = f2h(v);
-        } else if constexpr (EPI == EPI_F32) {
-            reinterpret_cast<float*>(C)[o] = v;
-        } else if constexpr (EPI == EPI_RESID) {
-            float* R = reinterpret_cast<float*>(C);
-            R[o] = R[o] + v;
-        } else if constexpr (EPI == EPI_BIAS) {
-            reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[n]));
-        } else {
-            reinterpret_cast<u16*>(C)[o] = f2h(v / (1.0f + expf(-v)) * u);
-        }
+}
+
+// Sums the S slices of a split skinny product in slice order, then the epilogue.
+template <int EPI>
+__global__ __launch_bounds__(256) void skinny_reduce(const float* __restrict__ part, int S, int M, int N, void* C,
+                                                     const u16* __restrict__ bias) {
+    constexpr int NP = EPI == EPI_SWIGLU ? 2 : 1;
+    const long e = (long)blockIdx.x * 256 + threadIdx.x, mn = (long)M * N;
+    if (e >= mn) return;
+    float v = 0.0f, u = 0.0f;
+    for (int ks = 0; ks < S; ks++) {
+        v += part[(size_t)ks * NP * mn + e];
+        if constexpr (NP == 2) u += part[(size_t)ks * NP * mn + mn + e];
+    }
+    sk_store<EPI>(C, bias, N, (int)(e / N), (int)(e % N), v, u);
+}
+
+// The skinny path's shape plan: 16-row tiles per workgroup and K slices.
+struct SkPlan {
+    bool use = false;
+    int rt = 1, split = 1;
+};
+SkPlan sk_plan(bool bt, int M, int N, int K) {
+    SkPlan p;
+    if (!bt || M <= 0 || M > 64 || N <= 0 || K <= 0 || K % 64) return p;
+    p.use = true;
+    p.rt = N >= 4096 ? 2 : 1;
+    const int blocks = (N + 16 * p.rt - 1) / (16 * p.rt), nst = K / 64;
+    // K slices only pay for their extra reduce launch when K is long and the
+    // row tiles alone leave most CUs idle.
+    if (blocks < 256 && nst >= 64) p.split = std::max(1, std::min(512 / blocks, nst / (2 * SK_WAVES)));
+    return p;
+}
+
+template <int EPI, int MT, int RT>
+void launch_skinny_rt(const u16* X, const u16* W, const u16* W2, void* C, const u16* bias, int M, int N, int K,
+                      int split, float* part, hipStream_t s) {
+    const unsigned blocks = (N + 16 * RT - 1) / (16 * RT);
+    if (split > 1) {
+        hipLaunchKernelGGL((gemm_skinny<EPI, MT, RT, true>), dim3(blocks, split), dim3(64 * SK_WAVES), 0, s, X, W, W2, C,
+                           bias, M, N, K, part);
+        const long mn = (long)M * N;
+        hipLaunchKernelGGL(skinny_reduce<EPI>, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, split, M, N,
+                           C, bias);
+    } else {
+        hipLaunchKernelGGL((gemm_skinny<EPI, MT, RT, false>), dim3(blocks), dim3(64 * SK_WAVES), 0, s, X, W, W2, C,
+                           bias, M, N, K, part);
     }
 }
 
 template <int EPI, int MT>
 void launch_skinny(const u16* X, const u16* W, const u16* W2, void* C, const u16* bias, int M, int N, int K,
-                   hipStream_t s) {
-    hipLaunchKernelGGL((gemm_skinny<EPI, MT>), dim3((N + 15) / 16), dim3(64 * SK_WAVES), 0, s, X, W, W2, C, bias, M, N,
-                       K);
+                   const SkPlan& p, float* part, hipStream_t s) {
+    if (p.rt == 2) launch_skinny_rt<EPI, MT, 2>(X, W, W2, C, bias, M, N, K, p.split, part, s);
+    else launch_skinny_rt<EPI, MT, 1>(X, W, W2, C, bias, M, N, K, p.split, part, s);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool BT, int EPI>
@@ -610,16 +693,17 @@ int run_gemm(const u16* A, const u16* B, const u16* B2, void* C, const u16* bias
 // a workgroup, else the smallest.
 template <bool BT, int EPI>
 int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16* bias, int M, int N, int K,
-                  hipStream_t s, const char* what) {
+                  hipStream_t s, const char* what, float* part = nullptr) {
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     constexpr bool DUAL = EPI == EPI_SWIGLU;
     if constexpr (BT) {
-        if (M > 0 && M <= 64 && N > 0 && K % 64 == 0) {  // a weight stream: the skinny path
+        const SkPlan p = sk_plan(true, M, N, K);
+        if (p.use && (p.split == 1 || part)) {  // a weight stream: the skinny path
             switch ((M + 15) / 16) {
-                case 1: launch_skinny<EPI, 1>(A, B, B2, C, bias, M, N, K, s); break;
-                case 2: launch_skinny<EPI, 2>(A, B, B2, C, bias, M, N, K, s); break;
-                case 3: launch_skinny<EPI, 3>(A, B, B2, C, bias, M, N, K, s); break;
-                default: launch_skinny<EPI, 4>(A, B, B2, C, bias, M, N, K, s); break;
+                case 1: launch_skinny<EPI, 1>(A, B, B2, C, bias, M, N, K, p, part, s); break;
+                case 2: launch_skinny<EPI, 2>(A, B, B2, C, bias, M, N, K, p, part, s); break;
+                case 3: launch_skinny<EPI, 3>(A, B, B2, C, bias, M, N, K, p, part, s); break;
+                default: launch_skinny<EPI, 4>(A, B, B2, C, bias, M, N, K, p, part, s); break;
             }
             return TSL_LAUNCHED(what);
         }
@@ -670,29 +754,43 @@ int launch_matmul_f32(TslKernel& k, const uint64_t* a, hipStream_t s) {
 int launch_linear_bias(TslKernel& k, const uint64_t* a, hipStream_t s) {
     int M = k.dim("M"), N = k.dim("N"), K = k.dim("K");
     return gemm_dispatch<true, EPI_BIAS>(P<u16>(a[0]), P<u16>(a[1]), nullptr, P<void>(a[3]), P<u16>(a[2]), M, N, K, s,
-                                         "linear");
+                                         "linear", reinterpret_cast<float*>(k.scratch));
 }
 
 int launch_llm_linear(TslKernel& k, const uint64_t* a, hipStream_t s) {
     int M = k.dim("M"), N = k.dim("N"), K = k.dim("K");
     return gemm_dispatch<true, EPI_F16>(P<u16>(a[0]), P<u16>(a[1]), nullptr, P<void>(a[2]), nullptr, M, N, K, s,
-                                        "linear");
+                                        "linear", reinterpret_cast<float*>(k.scratch));
 }
 
 int launch_linear_residual(TslKernel& k, const uint64_t* a, hipStream_t s) {
     int M = k.dim("M"), N = k.dim("N"), K = k.dim("K");
     return gemm_dispatch<true, EPI_RESID>(P<u16>(a[0]), P<u16>(a[1]), nullptr, P<void>(a[2]), nullptr, M, N, K, s,
-                                          "linear_residual");
+                                          "linear_residual", reinterpret_cast<float*>(k.scratch));
 }
 
 int launch_logits(TslKernel& k, const uint64_t* a, hipStream_t s) {
     int M = k.dim("M"), N = k.dim("N"), K = k.dim("K");
     return gemm_dispatch<true, EPI_F32>(P<u16>(a[0]), P<u16>(a[1]), nullptr, P<void>(a[2]), nullptr, M, N, K, s,
-                                        "logits");
+                                        "logits", reinterpret_cast<float*>(k.scratch));
 }
 
 int launch_gate_up(TslKernel& k, const uint64_t* a, hipStream_t s) {
     int M = k.dim("M"), F = k.dim("F"), K = k.dim("K");
     return gemm_dispatch<true, EPI_SWIGLU>(P<u16>(a[0]), P<u16>(a[1]), P<u16>(a[2]), P<void>(a[3]), nullptr, M, F, K,
-                                           s, "gate_up");
+                                           s, "gate_up", reinterpret_cast<float*>(k.scratch));
+}
+
+// Sizes the split-K partials of the skinny path (decode-sized M) once, when
+// the kernel is specialised: split x (2 for gate_up) x M x N floats.
+int prepare_projection(TslKernel& k) {
+    const bool dual = k.name == "gate_up";
+    const int64_t M = k.dim("M"), N = dual ? k.dim("F") : k.dim("N"), K = k.dim("K");
+    if (M > (1 << 20) || N > (1 << 30)) return 0;
+    const SkPlan p = sk_plan(true, (int)M, (int)N, (int)K);
+    if (!p.use || p.split == 1) return 0;
+    const size_t bytes = (size_t)p.split * (dual ? 2 : 1) * M * N * sizeof(float);
+    if (tsl_hip_check(hipMalloc(&k.scratch, bytes), "projection split-K scratch")) return -1;
+    k.scratch_bytes = bytes;
+    return 0;
 }

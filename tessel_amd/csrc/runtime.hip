@@ -46,6 +46,7 @@ int launch_decode_attention(TslKernel&, const uint64_t*, hipStream_t);
 int launch_paged_attention(TslKernel&, const uint64_t*, hipStream_t);
 int prepare_attention(TslKernel&);
 int prepare_decode(TslKernel&);
+int prepare_projection(TslKernel&);
 
 namespace {
 
@@ -83,7 +84,7 @@ std::vector<KernelDef> g_defs = {
     {"matmul", "matmul_f32", "A: f32[M, K], B: f32[K, N], C: f32[M, N]", "BM = 64, BN = 64, BK = 16", "",
      launch_matmul_f32, nullptr},
     {"matmul", "linear", "X: f16[M, K], W: f16[N, K], b: f16[N], Y: f16[M, N]", "BM = 64, BN = 128, BK = 32", "",
-     launch_linear_bias, nullptr},
+     launch_linear_bias, prepare_projection},
     {"attention", "flash_attention", "Q: f16[H, S, D], K: f16[H, S, D], V: f16[H, S, D], O: f16[H, S, D], scale: f32",
      "BM = 64, BN = 64", "D", launch_flash_attention, prepare_attention},
     {"attention", "paged_attention",
@@ -94,13 +95,13 @@ std::vector<KernelDef> g_defs = {
     {"llm", "rmsnorm", "X: f32[T, Dm], W: f16[Dm], Y: f16[T, Dm], eps: f32", "BR = 1, BC = 2048", "",
      launch_llm_rmsnorm, nullptr},
     {"llm", "linear", "X: f16[M, K], W: f16[N, K], Y: f16[M, N]", "BM = 16, BN = 64, BK = 64", "", launch_llm_linear,
-     nullptr},
+     prepare_projection},
     {"llm", "linear_residual", "X: f16[M, K], W: f16[N, K], R: f32[M, N]", "BM = 16, BN = 64, BK = 64", "",
-     launch_linear_residual, nullptr},
+     launch_linear_residual, prepare_projection},
     {"llm", "logits", "X: f16[M, K], W: f16[N, K], Y: f32[M, N]", "BM = 16, BN = 64, BK = 64", "", launch_logits,
-     nullptr},
+     prepare_projection},
     {"llm", "gate_up", "X: f16[M, K], Wg: f16[F, K], Wu: f16[F, K], Y: f16[M, F]", "BM = 16, BN = 64, BK = 64", "",
-     launch_gate_up, nullptr},
+     launch_gate_up, prepare_projection},
     {"llm", "rope_q", "QKV: f16[T, W], pos: i32[T], C: f32[NPOS, D2], S: f32[NPOS, D2], Q: f16[T, H, D]", "", "D2",
      launch_rope_q, nullptr},
     {"llm", "kv_write",
