@@ -273,8 +273,10 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     constexpr int TM = WM / 32, TN = WN / 32;     // 32x32 MFMA tiles per wave
     constexpr int LPA = BM / 8 / NW, LPB = BN / 8 / NW;  // 1 KB loads per wave per K step
     constexpr int RPL = 512 / BN;                 // B [K, N] rows per 1 KB load
-    static_assert(TM >= 1 && TN >= 1 && LPA >= 1 && LPB >= 1 && (BT || BN >= 128), "tile shape");
-    constexpr int STAGE = (BM + BN) * BK * 2;     // bytes per stage: A [BM][64], then B
+    constexpr bool DUAL = EPI == EPI_SWIGLU;      // gate_up: B and B2 share A
+    static_assert(TM >= 1 && TN >= 1 && LPA >= 1 && LPB >= 1 && (BT || BN >= 128) && (BT || !DUAL), "tile shape");
+    constexpr int BB = BN * BK * 2;               // bytes of one B tile
+    constexpr int STAGE = BM * BK * 2 + (DUAL ? 2 : 1) * BB;  // bytes per stage: A [BM][64], then B (, B2)
     __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE / 2];
 
     const int lane = threadIdx.x & 63;
@@ -320,8 +322,9 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         // Resources whose base is the step's first column (A) / row (B).
         const long a_shift = (long)k0 * 2, b_shift = BT ? (long)k0 * 2 : (long)k0 * N * 2;
         const i32x4 ra = make_rsrc(reinterpret_cast<const char*>(A) + a_shift, (uint32_t)((long)M * K * 2 - a_shift));
-        const i32x4 rb = make_rsrc(reinterpret_cast<const char*>(B) + b_shift,
-                                   (uint32_t)((BT ? (long)N * K : (long)K * N) * 2 - b_shift));
+        const uint32_t b_range = (uint32_t)((BT ? (long)N * K : (long)K * N) * 2 - b_shift);
+        const i32x4 rb = make_rsrc(reinterpret_cast<const char*>(B) + b_shift, b_range);
+        const i32x4 rb2 = make_rsrc(reinterpret_cast<const char*>(DUAL ? B2 : B) + b_shift, b_range);
         const uint32_t sa = lds_base + stage * STAGE + wave * LPA * 1024;
         const uint32_t sb = lds_base + stage * STAGE + BM * BK * 2 + wave * LPB * 1024;
         if (k0 + BK <= K) {  // every k of the step exists (uniform)
@@ -333,6 +336,11 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
             for (int i = 0; i < LPB; i++)
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sb + i * 1024),
                              "v"(offb[i]), "s"(rb));
+            if constexpr (DUAL)
+#pragma unroll
+                for (int i = 0; i < LPB; i++)
+                    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sb + BB + i * 1024),
+                                 "v"(offb[i]), "s"(rb2));
         } else {
 #pragma unroll
             for (int i = 0; i < LPA; i++) {
@@ -345,6 +353,9 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
                 const uint32_t v = k0 + kb[i] < K ? offb[i] : (uint32_t)OOB;
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sb + i * 1024),
                              "v"(v), "s"(rb));
+                if constexpr (DUAL)
+                    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sb + BB + i * 1024),
+                                 "v"(v), "s"(rb2));
             }
         }
     };
@@ -370,14 +381,16 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         }
     }
     const char* ldsc = reinterpret_cast<const char*>(lds);
-    auto read_ops = [&](int so, int st, half8* av, half8* bv) {
+    auto read_ops = [&](int so, int st, half8* av, half8* bv, half8* bv2) {
 #pragma unroll
         for (int i = 0; i < TM; i++) av[i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 4096);
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             if constexpr (BT) {
                 const int r = wn0 + j * 32 + (lane & 31);
-                bv[j] = *reinterpret_cast<const half8*>(ldsc + so + b_addr[j] + (((2 * st + g) ^ ((r >> 1) & 7)) * 16));
+                const int cb = so + b_addr[j] + (((2 * st + g) ^ ((r >> 1) & 7)) * 16);
+                bv[j] = *reinterpret_cast<const half8*>(ldsc + cb);
+                if constexpr (DUAL) bv2[j] = *reinterpret_cast<const half8*>(ldsc + cb + BB);
             } else {
                 const half4 h0 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + (16 * st) * BN * 2));
                 const half4 h1 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + (16 * st + 4) * BN * 2));
@@ -386,36 +399,46 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         }
     };
 
-    float16v acc[TM][TN];
+    float16v acc[TM][TN], acc2[DUAL ? TM : 1][DUAL ? TN : 1];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = float16v{};
+    if constexpr (DUAL)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc2[i][j] = float16v{};
 
     const int nk = (K + BK - 1) / BK;
     issue(0, 0);
-    half8 a0[TM], b0[TN], a1[TM], b1[TN];
+    half8 a0[TM], b0[TN], a1[TM], b1[TN], c0[DUAL ? TN : 1], c1[DUAL ? TN : 1];
     for (int kt = 0; kt < nk; kt++) {
         const int stage = kt & 1;
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of step kt are in LDS
         __syncthreads();                     // everyone's; and step kt-1 is done reading the other stage
         if (kt + 1 < nk) issue((kt + 1) * BK, stage ^ 1);
         const int so = stage * STAGE;
-        read_ops(so, 0, a0, b0);
+        read_ops(so, 0, a0, b0, c0);
 #pragma unroll
         for (int st = 0; st < BK / 16; st++) {
             half8* av = (st & 1) ? a1 : a0;
             half8* bv = (st & 1) ? b1 : b0;
-            if (st + 1 < BK / 16) read_ops(so, st + 1, (st & 1) ? a0 : a1, (st & 1) ? b0 : b1);
+            half8* cv = (st & 1) ? c1 : c0;
+            if (st + 1 < BK / 16) read_ops(so, st + 1, (st & 1) ? a0 : a1, (st & 1) ? b0 : b1, (st & 1) ? c0 : c1);
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
-                for (int j = 0; j < TN; j++)
+                for (int j = 0; j < TN; j++) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+                    if constexpr (DUAL)
+                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], cv[j], acc2[i][j], 0, 0, 0);
+                }
         }
         // Pin the schedule: step 0's operand reads, then per k-step the next
         // step's reads spread over its first MFMAs, the rest back to back.
-        constexpr int NRD = BT ? TM + TN : TM + 2 * TN;  // LDS reads per k-step
+        constexpr int NRD = BT ? TM + (DUAL ? 2 : 1) * TN : TM + 2 * TN;  // LDS reads per k-step
+        constexpr int NMF = (DUAL ? 2 : 1) * TM * TN;                    // MFMAs per k-step
         __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
 #pragma unroll
         for (int st = 0; st < BK / 16; st++) {
@@ -425,9 +448,9 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - NRD / 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD / 2, 0);
             } else {
-                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, NMF, 0);
             }
         }
     }
@@ -451,8 +474,11 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
                 } else if constexpr (EPI == EPI_RESID) {
                     float* R = reinterpret_cast<float*>(C);
                     R[o] = R[o] + v;
-                } else {
+                } else if constexpr (EPI == EPI_BIAS) {
                     reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
+                } else {
+                    const float u = acc2[DUAL ? i : 0][DUAL ? j : 0][r];
+                    reinterpret_cast<u16*>(C)[o] = f2h(v / (1.0f + expf(-v)) * u);
                 }
             }
         }
@@ -708,9 +734,8 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             return TSL_LAUNCHED(what);
         }
     }
+    const bool aligned = (K % 8) == 0 && (BT || (N % 8) == 0) && (long)M * K < (1L << 30) && (long)N * K < (1L << 30);
     if constexpr (!DUAL) {
-        const bool aligned = (K % 8) == 0 && (BT || (N % 8) == 0) && (long)M * K < (1L << 30) &&
-                             (long)N * K < (1L << 30);
         if (tiles(256, 256) >= 224 && aligned) {
             // 8 wavefronts of 128 x 64 (2 per SIMD, 128 accumulator registers
             // each): one wave's MFMAs cover the other's loads and barrier.
@@ -718,13 +743,19 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
                                C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
-        if (aligned && M > 64) {
+    }
+    if (aligned && M > 64 && (BT || !DUAL)) {
+        if (tiles(128, 128) >= 256) {
             hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
-            return TSL_LAUNCHED(what);
+        } else {  // 64 x 128 tiles (4 wavefronts of 64 x 32): twice the workgroups
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 128, 1, 4>), dim3(tiles(64, 128)), dim3(256), 0, s, A, B, B2, C,
+                               bias, M, N, K, 4);
         }
-        if (tiles(256, 256) >= 224) return run_gemm<256, 256, 64, 2, 2, BT, EPI>(A, B, B2, C, bias, M, N, K, s, what);
+        return TSL_LAUNCHED(what);
     }
+    if constexpr (!DUAL)
+        if (tiles(256, 256) >= 224) return run_gemm<256, 256, 64, 2, 2, BT, EPI>(A, B, B2, C, bias, M, N, K, s, what);
     if (tiles(128, 128) >= 224 || M > 64) return run_gemm<128, 128, 64, 2, 2, BT, EPI>(A, B, B2, C, bias, M, N, K, s, what);
     if (M > 32) return run_gemm<64, 64, 64, 2, 2, BT, EPI>(A, B, B2, C, bias, M, N, K, s, what);
     return run_gemm<32, 64, 64, 1, 2, BT, EPI>(A, B, B2, C, bias, M, N, K, s, what);
