@@ -31,6 +31,7 @@ struct AttnArgs {
     u16* O;
     const int* starts;  // prefill only
     int S, H, G;
+    int ncu;  // compute units (workgroups dispatched round-robin over them)
     long q_row, q_head, k_row, k_head;  // element strides
     float scale;
 };
@@ -83,8 +84,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nqb = (a.S + BQ - 1) / BQ;
-    const int qb = nqb - 1 - (int)(blockIdx.x / a.H);
-    const int h = blockIdx.x % a.H;
+    // Work rank (0 = most keys): longest first, and within every full round of
+    // NCU workgroups (one per CU) alternately reversed, so the workgroups
+    // sharing a CU (ranks j, 2 NCU-1-j, 2 NCU+j, ...) add up to the same work.
+    int rank = blockIdx.x;
+    {
+        const int r = rank / a.ncu, j = rank % a.ncu;
+        if ((r & 1) && (r + 1) * a.ncu <= (int)gridDim.x) rank = r * a.ncu + a.ncu - 1 - j;
+    }
+    const int qb = nqb - 1 - rank / a.H;
+    const int h = rank % a.H;
     const int hk = PREFILL ? h / (a.H / a.G) : h;
     const int q0 = qb * BQ, qw = q0 + wave * 32;
     const int myq = qw + (lane & 31);
@@ -269,9 +278,23 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     }
 }
 
+int num_cus() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
 template <bool PREFILL>
-int run_attn(const AttnArgs& a, int D, hipStream_t s, const char* what) {
+int run_attn(AttnArgs a, int D, hipStream_t s, const char* what) {
     if (a.S == 0 || a.H == 0) return 0;
+    a.ncu = num_cus();
     dim3 grid(((a.S + BQ - 1) / BQ) * a.H);
     switch (D) {
         case 16: hipLaunchKernelGGL((attn_fwd<16, PREFILL>), grid, dim3(256), 0, s, a); break;
