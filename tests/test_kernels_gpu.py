@@ -114,7 +114,7 @@ def test_every_tuning_candidate(name, m):
         parity(f"{name} m={m} {meta}", got, want)
 
 
-@pytest.mark.parametrize("m", [1, 16, 32, 128, 512])
+@pytest.mark.parametrize("m", [1, 16, 32, 48, 64, 128, 512])
 @pytest.mark.parametrize("name", MM_CASES)
 def test_llm_matmuls_tinyllama_shapes(name, m):
     _say("llm mm", name, m)
@@ -124,6 +124,30 @@ def test_llm_matmuls_tinyllama_shapes(name, m):
     args, want = _mm_args(r, name, m, k, n, wscale=1.0 / np.sqrt(k))
     got = T.run("llm", name, args, outputs=[len(args) - 1])[len(args) - 1]
     parity(f"{name} m={m}", got, want)
+
+
+@pytest.mark.parametrize("name", MM_CASES)
+@pytest.mark.parametrize("m,k,n", [(40, 192, 100), (7, 4160, 33), (64, 64, 1)])
+def test_llm_matmuls_ragged_few_rows(name, m, k, n):
+    # Few-row (decode-sized) products with ragged M and N, one K step, and a
+    # long K that is split across workgroups.
+    _say("llm mm ragged", name, m, k, n)
+    r = oracle.Rng(300 + m + n)
+    args, want = _mm_args(r, name, m, k, n, wscale=1.0 / np.sqrt(k))
+    got = T.run("llm", name, args, outputs=[len(args) - 1])[len(args) - 1]
+    parity(f"{name} {m}x{k}x{n}", got, want)
+
+
+def test_split_k_products_repeat_bit_identically():
+    # The K-split partials are summed in slice order: repeated launches agree
+    # bit for bit.
+    _say("split-k repeat")
+    r = oracle.Rng(77)
+    args, want = _mm_args(r, "linear", 32, 5632, 2048, wscale=1.0 / np.sqrt(5632))
+    outs = [T.run("llm", "linear", [a.copy() for a in args], outputs=[2])[2] for _ in range(3)]
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.view(np.uint16), outs[0].view(np.uint16))
+    parity("split-k linear", outs[0], want)
 
 
 # ---------------------------------------------------------------- attention
