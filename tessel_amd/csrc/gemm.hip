@@ -242,6 +242,9 @@ constexpr int OOB = 0x7fffffff;              // a byte offset past any range
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+// s_waitcnt immediate for vmcnt(n) alone (6-bit vmcnt: bits 3:0 and 15:14).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0f70; }
+
 // A buffer resource (base, byte range, gfx9 flags) for buffer loads.
 TSL_DEV i32x4 make_rsrc(const void* p, uint32_t bytes) {
     const uint64_t a = reinterpret_cast<uint64_t>(p);
@@ -262,22 +265,27 @@ TSL_DEV half4 lds_read_tr(const u16* p) {
 // operand read cover all 16 slots of the 256-byte bank window); B row k (NN)
 // holds logical chunk c at c ^ ((k & 3) << 2), so the 4 k rows x 2 column
 // halves a 32-lane transposed read touches are 8 distinct 32-byte granules.
-template <bool BT, int EPI, int BM, int BN, int WGM, int WGN>
+template <bool BT, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS>
 __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restrict__ A, const u16* __restrict__ B,
                                                              const u16* __restrict__ B2, void* __restrict__ C,
                                                              const u16* __restrict__ bias, int M, int N, int K,
                                                              int G) {
-    constexpr int BK = 64, KC = BK / 8;
+    constexpr int KC = BK / 8;                    // 16-byte chunks per LDS row of A (and W)
+    static_assert((BK == 64 || BK == 32) && NS >= 2 && NS <= 4, "k step and stages");
     constexpr int NW = WGM * WGN;                 // wavefronts: WGM x WGN, each (BM/WGM) x (BN/WGN)
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;     // 32x32 MFMA tiles per wave
-    constexpr int LPA = BM / 8 / NW, LPB = BN / 8 / NW;  // 1 KB loads per wave per K step
+    constexpr int LPA = BM * BK / 512 / NW, LPB = BN * BK / 512 / NW;  // 1 KB loads per wave per K step
     constexpr int RPL = 512 / BN;                 // B [K, N] rows per 1 KB load
+    constexpr int RPA = 512 / BK;                 // A (W) rows per 1 KB load
     constexpr bool DUAL = EPI == EPI_SWIGLU;      // gate_up: B and B2 share A
     static_assert(TM >= 1 && TN >= 1 && LPA >= 1 && LPB >= 1 && (BT || BN >= 128) && (BT || !DUAL), "tile shape");
     constexpr int BB = BN * BK * 2;               // bytes of one B tile
-    constexpr int STAGE = BM * BK * 2 + (DUAL ? 2 : 1) * BB;  // bytes per stage: A [BM][64], then B (, B2)
-    __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE / 2];
+    constexpr int STAGE = BM * BK * 2 + (DUAL ? 2 : 1) * BB;  // bytes per stage: A [BM][BK], then B (, B2)
+    constexpr int LPS = LPA + (DUAL ? 2 : 1) * LPB;          // loads per wave per stage
+    __shared__ __attribute__((aligned(16))) u16 lds[NS * STAGE / 2];
+    // Row r of an A (W) tile holds logical 16-byte chunk c at c ^ sw(r).
+    auto sw = [](int r) { return KC == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -297,8 +305,8 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
 #pragma unroll
     for (int i = 0; i < LPA; i++) {
         const int q = wave * LPA + i;
-        const int r = 8 * q + (lane >> 3);
-        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int r = RPA * q + lane / KC;
+        const int c = (lane % KC) ^ sw(r);
         ka[i] = 8 * c;
         offa[i] = m0 + r < M ? (uint32_t)(((m0 + r) * K + 8 * c) * 2) : (uint32_t)OOB;
     }
@@ -306,8 +314,8 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     for (int i = 0; i < LPB; i++) {
         const int q = wave * LPB + i;
         if constexpr (BT) {
-            const int r = 8 * q + (lane >> 3);
-            const int c = (lane & 7) ^ ((r >> 1) & 7);
+            const int r = RPA * q + lane / KC;
+            const int c = (lane % KC) ^ sw(r);
             kb[i] = 8 * c;
             offb[i] = n0 + r < N ? (uint32_t)(((n0 + r) * K + 8 * c) * 2) : (uint32_t)OOB;
         } else {
@@ -362,11 +370,11 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
 
     // LDS byte addresses of this lane's operands in stage 0: A at k-step s,
     // tile i: a_addr[s] + 4096 i; B (NN) tile j: b_addr[j] + (16 s + 4 h) 512.
-    uint32_t a_addr[4], b_addr[TN];
+    uint32_t a_addr[BK / 16], b_addr[TN];
 #pragma unroll
-    for (int st = 0; st < 4; st++) {
+    for (int st = 0; st < BK / 16; st++) {
         const int r = wm0 + (lane & 31);
-        a_addr[st] = (uint32_t)((r * KC + ((2 * st + g) ^ ((r >> 1) & 7))) * 16);
+        a_addr[st] = (uint32_t)((r * KC + ((2 * st + g) ^ sw(r))) * 16);
     }
 #pragma unroll
     for (int j = 0; j < TN; j++) {
@@ -383,12 +391,12 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     const char* ldsc = reinterpret_cast<const char*>(lds);
     auto read_ops = [&](int so, int st, half8* av, half8* bv, half8* bv2) {
 #pragma unroll
-        for (int i = 0; i < TM; i++) av[i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 4096);
+        for (int i = 0; i < TM; i++) av[i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 32 * BK * 2);
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             if constexpr (BT) {
                 const int r = wn0 + j * 32 + (lane & 31);
-                const int cb = so + b_addr[j] + (((2 * st + g) ^ ((r >> 1) & 7)) * 16);
+                const int cb = so + b_addr[j] + (((2 * st + g) ^ sw(r)) * 16);
                 bv[j] = *reinterpret_cast<const half8*>(ldsc + cb);
                 if constexpr (DUAL) bv2[j] = *reinterpret_cast<const half8*>(ldsc + cb + BB);
             } else {
@@ -410,15 +418,23 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
 #pragma unroll
             for (int j = 0; j < TN; j++) acc2[i][j] = float16v{};
 
+    // NS stages in a ring, NS - 1 k steps in flight: iteration kt waits for
+    // step kt (this wave's loads of later steps may still run), syncs (every
+    // wave's loads have landed, and step kt-1's reads of its stage are done),
+    // then refills that stage with step kt + NS - 1.
     const int nk = (K + BK - 1) / BK;
-    issue(0, 0);
+    for (int p = 0; p < NS - 1 && p < nk; p++) issue(p * BK, p);
     half8 a0[TM], b0[TN], a1[TM], b1[TN], c0[DUAL ? TN : 1], c1[DUAL ? TN : 1];
+    int stage = 0;
     for (int kt = 0; kt < nk; kt++) {
-        const int stage = kt & 1;
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of step kt are in LDS
-        __syncthreads();                     // everyone's; and step kt-1 is done reading the other stage
-        if (kt + 1 < nk) issue((kt + 1) * BK, stage ^ 1);
+        const int ahead = min(NS - 2, nk - 1 - kt);  // steps after kt already issued
+        if (ahead <= 0) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPS));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPS));
+        __syncthreads();
+        if (kt + NS - 1 < nk) issue((kt + NS - 1) * BK, stage == 0 ? NS - 1 : stage - 1);
         const int so = stage * STAGE;
+        stage = stage + 1 == NS ? 0 : stage + 1;
         read_ops(so, 0, a0, b0, c0);
 #pragma unroll
         for (int st = 0; st < BK / 16; st++) {
@@ -739,17 +755,17 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
         if (tiles(256, 256) >= 224 && aligned) {
             // 8 wavefronts of 128 x 64 (2 per SIMD, 128 accumulator registers
             // each): one wave's MFMAs cover the other's loads and barrier.
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, B2,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4, 64, 2>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
     }
     if (aligned && M > 64 && (BT || !DUAL)) {
         if (tiles(128, 128) >= 256) {
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
         } else {  // 64 x 128 tiles (4 wavefronts of 64 x 32): twice the workgroups
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 128, 1, 4>), dim3(tiles(64, 128)), dim3(256), 0, s, A, B, B2, C,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 128, 1, 4, 64, 2>), dim3(tiles(64, 128)), dim3(256), 0, s, A, B, B2, C,
                                bias, M, N, K, 4);
         }
         return TSL_LAUNCHED(what);
