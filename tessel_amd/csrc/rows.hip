@@ -96,14 +96,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ X, 
     u16* y = Y + (size_t)row * C;
     const bool vec = (C % E) == 0;
     float v[NV][E];
-    // This lane's weights, fetched alongside x (independent of the sum).
-    typedef uint32_t wvec __attribute__((ext_vector_type(E / 2)));
-    wvec wv[NV];
-#pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int c = (i * 64 + lane) * E;
-        if (vec && c + E <= ncols) wv[i] = *reinterpret_cast<const wvec*>(W + c);
-    }
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
@@ -137,9 +129,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ X, 
             // E outputs: 8 halves (16 bytes) for f16 input rows, 4 (8 bytes) for f32.
             uint32_t o[E / 2];
             for (int p = 0; p < E / 2; p++) {
-                const uint32_t wp = wv[i][p];
-                u16 lo = f2h(v[i][2 * p] * rs * h2f((u16)(wp & 0xffff)));
-                u16 hi = f2h(v[i][2 * p + 1] * rs * h2f((u16)(wp >> 16)));
+                u16 lo = f2h(v[i][2 * p] * rs * h2f(W[c + 2 * p]));
+                u16 hi = f2h(v[i][2 * p + 1] * rs * h2f(W[c + 2 * p + 1]));
                 o[p] = (uint32_t)lo | ((uint32_t)hi << 16);
             }
             if constexpr (E == 8) {
