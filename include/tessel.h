@@ -148,6 +148,40 @@ typedef struct {
 int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* offsets, const int32_t* max_new,
                  int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats);
 
+/* ---- checkpoints (src/llm/safetensors.rs) */
+
+/* The shape of a Hugging Face Llama-family checkpoint directory, from its
+ * config.json (src/llm/safetensors.rs:190-226 config): required
+ * hidden_size, num_hidden_layers, num_attention_heads, intermediate_size,
+ * vocab_size; num_key_value_heads, head_dim, rms_norm_eps (1e-6),
+ * rope_theta (10000), max_position_embeddings (2048, capped at 8192),
+ * bos_token_id (1), eos_token_id (a number or the first of a list, else -1)
+ * default as there; a non-null rope_scaling is an error. */
+int tsl_checkpoint_config(const char* dir, tsl_config* cfg);
+/* Its tensors (model.safetensors, else the shards that
+ * model.safetensors.index.json lists) as f16 bits in the layout of
+ * tsl_weights_random; F16 is copied, BF16 and F32 are rounded to nearest
+ * even. q/k/v projections are stacked into wqkv. *has_head is 0 when there
+ * is no lm_head.weight (head untouched: tie it to embed), else head is
+ * filled. Biases, missing tensors, other shapes and other dtypes are
+ * errors, reported as the reference words them
+ * (src/llm/safetensors.rs:229-358 index/read/load). cfg must be the
+ * directory's tsl_checkpoint_config. */
+int tsl_checkpoint_load(const char* dir, const tsl_config* cfg, uint16_t* embed, uint16_t* layers, uint16_t* norm,
+                        uint16_t* head, int* has_head);
+/* Writes weights (the tsl_weights_random layout; head NULL: tied) as a
+ * checkpoint directory that exists already: config.json and one F16
+ * model.safetensors laid out as Hugging Face lays one out
+ * (src/llm/safetensors.rs:362-444 save). */
+int tsl_checkpoint_save(const char* dir, const tsl_config* cfg, const uint16_t* embed, const uint16_t* layers,
+                        const uint16_t* norm, const uint16_t* head);
+/* The checkpoint reader's JSON parser (src/llm/safetensors.rs:44-187
+ * parse_json): text parsed and written back normalised (members in file
+ * order, strings unescaped then re-escaped, numbers shortest round-trip);
+ * *len gets its length, out the text when cap > *len. A syntax error
+ * returns TSL_ERR_ARG with the byte offset in the message. */
+int tsl_json_roundtrip(const char* text, char* out, size_t cap, size_t* len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,7 +45,8 @@ EXPORTS = [
     "tsl_free", "tsl_upload", "tsl_download", "tsl_fill_nan", "tsl_kernel", "tsl_kernel_key", "tsl_launch",
     "tsl_time_launches", "tsl_capture_begin", "tsl_capture_end", "tsl_replay", "tsl_event_record",
     "tsl_event_elapsed", "tsl_weights_sizes", "tsl_weights_random", "tsl_engine_new", "tsl_engine_free",
-    "tsl_engine_set", "tsl_engine_step", "tsl_generate",
+    "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
+    "tsl_checkpoint_save", "tsl_json_roundtrip",
 ]
 
 
@@ -110,6 +111,10 @@ def _declare(L):
     L.tsl_engine_set.argtypes = [_INT, _INT, _INT]
     L.tsl_engine_step.argtypes = [_INT, _INT, _P, _P, _P, _INT, _P, _INT, _P, _P, _INT, _P, _P]
     L.tsl_generate.argtypes = [_INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, ctypes.POINTER(Stats)]
+    L.tsl_checkpoint_config.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config)]
+    L.tsl_checkpoint_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config), _P, _P, _P, _P, ctypes.POINTER(_INT)]
+    L.tsl_checkpoint_save.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config), _P, _P, _P, _P]
+    L.tsl_json_roundtrip.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
 
 
 def check(rc):
@@ -322,6 +327,54 @@ def weights_random(cfg, seed):
     check(lib().tsl_weights_random(ctypes.byref(cfg), int(seed), embed.ctypes.data, layers.ctypes.data,
                                    norm.ctypes.data, head.ctypes.data))
     return embed, layers, norm, head
+
+
+def checkpoint_config(path):
+    """safetensors::config (src/llm/safetensors.rs:190-226): the Config of a
+    Hugging Face checkpoint directory."""
+    cfg = Config()
+    check(lib().tsl_checkpoint_config(os.fsencode(path), ctypes.byref(cfg)))
+    return cfg
+
+
+def load_checkpoint(path):
+    """safetensors::load (src/llm/safetensors.rs:324-358): (cfg, (embed,
+    layers, norm, head)) with head None when the checkpoint ties it to the
+    embedding; arrays in the weights_random layout, float16."""
+    cfg = checkpoint_config(path)
+    sz = [ctypes.c_size_t() for _ in range(4)]
+    check(lib().tsl_weights_sizes(ctypes.byref(cfg), *[ctypes.byref(s) for s in sz]))
+    embed = np.zeros(sz[0].value, np.float16)
+    layers = np.zeros(sz[1].value * cfg.layers, np.float16)
+    norm = np.zeros(sz[2].value, np.float16)
+    head = np.zeros(sz[3].value, np.float16)
+    has = _INT()
+    check(lib().tsl_checkpoint_load(os.fsencode(path), ctypes.byref(cfg), embed.ctypes.data, layers.ctypes.data,
+                                    norm.ctypes.data, head.ctypes.data, ctypes.byref(has)))
+    return cfg, (embed, layers, norm, head if has.value else None)
+
+
+def save_checkpoint(path, cfg, weights):
+    """safetensors::save (src/llm/safetensors.rs:362-444): config.json and one
+    F16 model.safetensors under the directory `path` (created if needed);
+    weights = (embed, layers, norm, head or None)."""
+    os.makedirs(path, exist_ok=True)
+    embed, layers, norm, head = weights
+    arrs = [np.ascontiguousarray(a, np.float16) for a in (embed, layers, norm)]
+    h = None if head is None else np.ascontiguousarray(head, np.float16)
+    check(lib().tsl_checkpoint_save(os.fsencode(path), ctypes.byref(cfg), arrs[0].ctypes.data, arrs[1].ctypes.data,
+                                    arrs[2].ctypes.data, None if h is None else h.ctypes.data))
+
+
+def json_roundtrip(text):
+    """The checkpoint reader's JSON parser, parsed then written back (a syntax
+    error raises TesselError)."""
+    b = text.encode("utf-8")
+    n = ctypes.c_size_t()
+    check(lib().tsl_json_roundtrip(b, None, 0, ctypes.byref(n)))
+    buf = ctypes.create_string_buffer(n.value + 1)
+    check(lib().tsl_json_roundtrip(b, buf, n.value + 1, ctypes.byref(n)))
+    return buf.value.decode("utf-8")
 
 
 def _i32(a):

@@ -22,7 +22,7 @@ HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-Wall", "-
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall"]
 
 SOURCES = ["runtime.hip", "gemm.hip", "attention.hip", "decode.hip", "rows.hip"]
-HOST_SOURCES = ["engine.cpp"]
+HOST_SOURCES = ["engine.cpp", "checkpoint.cpp"]
 
 
 def _compile(cmd):

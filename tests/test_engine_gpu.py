@@ -77,3 +77,33 @@ def test_graph_replay_matches_eager(gpu):
         outs.append(e.generate(reqs, 3)[0])
         e.close()
     assert outs[0] == outs[1]
+
+
+def test_engine_from_a_bf16_checkpoint(gpu, tmp_path):
+    # A checkpoint as another writer stores it (BF16, Hugging Face names),
+    # read by the loader, runs through the engine like the reference model
+    # with the same (converted) weights.
+    import json
+    import torch
+    from safetensors.torch import save_file
+    cfg = T.Config.tiny()
+    w = T.weights_random(cfg, 9)
+    T.save_checkpoint(str(tmp_path / "f16"), cfg, w)
+    from safetensors.torch import load_file
+    t = load_file(str(tmp_path / "f16" / "model.safetensors"))
+    save_file({k: v.to(torch.float32).to(torch.bfloat16) for k, v in t.items()}, str(tmp_path / "model.safetensors"))
+    with open(tmp_path / "f16" / "config.json") as f:
+        conf = json.load(f)
+    with open(tmp_path / "config.json", "w") as f:
+        json.dump(conf, f)
+    c2, w2 = T.load_checkpoint(str(tmp_path))
+    assert w2[3] is not None
+    e = T.Engine(c2, limits(), w2)
+    prompt = [1, 7, 99, 42, 3, 128, 200]
+    n = len(prompt)
+    got = e.step(prompt, list(range(n)), list(range(n)), T.Engine.PREFILL, want=[n - 1])
+    want = oracle.forward(oracle.Config.tiny(), w2, prompt)
+    err = rel(got[0], want[n - 1])
+    print(f"bf16 checkpoint prefill: logits within {err:.2e} of the reference", flush=True)
+    assert err < 2e-2
+    e.close()
