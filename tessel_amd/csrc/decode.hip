@@ -331,9 +331,10 @@ __global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
         const uint32_t sk = lds0 + st * WSTAGE, sv = sk + TILE;
 #pragma unroll
         for (int q = 0; q < NLD; q++) {
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sk + q * 1024),
+            // K and V are read once: nontemporal (streamed past the caches).
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(sk + q * 1024),
                          "v"(offk[q]), "s"(rk));
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sv + q * 1024),
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(sv + q * 1024),
                          "v"(offv[q]), "s"(rv));
         }
     };
