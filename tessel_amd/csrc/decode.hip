@@ -20,7 +20,8 @@
 namespace {
 
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr int DEC_MAX_CHUNK = 16;  // pages per workgroup, at most (one table entry per lane)
+constexpr int DEC_MAX_CHUNK = 16;  // pages per chunk of a long table, at most
+constexpr int DEC_WIDE_MAX_PAGES = 64;  // tables up to this many pages: one chunk per sequence
 
 struct DecArgs {
     const u16* Q;
@@ -217,8 +218,10 @@ __global__ __launch_bounds__(64) void decode_combine(DecArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Matrix-core path (D = 64 or 128, P a multiple of 16). A single-wavefront
-// workgroup owns (b, kv head g, chunk of CH pages) and walks its
+// Matrix-core path (D = 64 or 128, P a multiple of 16). A workgroup owns
+// (b, kv head g, chunk of CH pages): one wavefront for the chunks of a long
+// table, NWV of them (tiles w, w + NWV, ...; states merged in LDS) when the
+// whole table is one chunk. A wavefront walks its
 // 16-token tiles through a DEC_STAGES-deep ring of LDS stages, each filled by
 // direct buffer->LDS loads (K rows then V rows, 16 x 2D bytes each), so that
 // DEC_STAGES - 1 tiles are in flight while one is computed. Per tile:
@@ -266,8 +269,8 @@ TSL_DEV void wait_tiles(int tiles) {
     }
 }
 
-template <int D, int QPG>
-__global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
+template <int D, int QPG, int NWV>
+__global__ __launch_bounds__(64 * NWV) void decode_tiles(DecArgs a) {
     constexpr int ROWB = 2 * D, KCH = D / 8;
     constexpr int TILE = TT * ROWB;   // bytes of K (or V) per tile
     constexpr int NLD = TILE / 1024;  // 1 KB loads per matrix per tile
@@ -275,9 +278,10 @@ __global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
     constexpr int WSTAGE = 2 * TILE;  // K then V
     constexpr float LAZY = 8.0f;
     static_assert(DEC_STAGES >= 2 && DEC_STAGES <= 4, "wait_tiles covers up to 3 tiles in flight");
-    __shared__ __attribute__((aligned(16))) char lds[DEC_STAGES * WSTAGE];
+    __shared__ __attribute__((aligned(16))) char lds[NWV * DEC_STAGES * WSTAGE];  // a ring per wavefront
 
-    const int lane = threadIdx.x, grp = lane >> 4, col = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, col = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // The kv heads of one (b, chunk) are adjacent in launch order, so the
     // pages' token rows (all G heads' 2D-byte slices) are read at one time.
     const int g = blockIdx.x % a.G, c = (blockIdx.x / a.G) % a.NCH, b = blockIdx.x / (a.G * a.NCH);
@@ -286,13 +290,14 @@ __global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
     const int nact = min((npages + a.CH - 1) / a.CH, a.NCH);
     if (c >= nact) {
         if (c == 0)  // lens 0: 0 / 0, as the .tl computes
-            for (int x = lane; x < QPG * D; x += 64) a.O[((long)b * a.H + g * QPG) * D + x] = f2h(0.0f / 0.0f);
+            for (int x = tid; x < QPG * D; x += 64 * NWV) a.O[((long)b * a.H + g * QPG) * D + x] = f2h(0.0f / 0.0f);
         return;
     }
     const int t_lo = c * a.CH * a.P;
     const int t_hi = c == a.NCH - 1 ? n : min(n, (c + 1) * a.CH * a.P);
     const int t_end = (t_hi + a.P - 1) / a.P * a.P;  // through the last page
-    const int nt = (t_end - t_lo) / TT;
+    const int ntile = (t_end - t_lo) / TT;
+    const int nt = wave < ntile ? (ntile - wave + NWV - 1) / NWV : 0;  // tiles wave, wave + NWV, ...
 
     // Q^T operand: lane l holds head l%16, d = 32 s + 8 (l/16) .. +8.
     half8 qop[D / 32];
@@ -317,11 +322,11 @@ __global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
         offk[q] = (uint32_t)(row * tok_bytes + ((pc ^ tswz_k<D>(row)) * 16));
         offv[q] = (uint32_t)(row * tok_bytes + ((pc ^ tswz_v<D>(row)) * 16));
     }
-    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds) + wave * DEC_STAGES * WSTAGE;
     const char* Kg = reinterpret_cast<const char*>(a.Kc) + (long)g * D * 2;
     const char* Vg = reinterpret_cast<const char*>(a.Vc) + (long)g * D * 2;
-    auto issue = [&](int ti, int st) {
-        const int t0 = t_lo + ti * TT;
+    auto issue = [&](int i, int st) {  // this wave's i-th tile
+        const int t0 = t_lo + (wave + NWV * i) * TT;
         const int pi = t0 >> a.pshift;
         const int page = pi < a.MP ? __builtin_amdgcn_readlane(tab, pi - page_lo) : 0;
         const bool ok = page >= 0 && page < a.NP;  // outside the pool: zeros
@@ -372,7 +377,7 @@ __global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
             issue(i + DEC_STAGES - 1, sn >= DEC_STAGES ? sn - DEC_STAGES : sn);
         }
         wait_tiles<NLD>(min(nt - 1 - i, DEC_STAGES - 1));  // tile i has landed
-        const char* sb = lds + st * WSTAGE;
+        const char* sb = lds + (wave * DEC_STAGES + st) * WSTAGE;
         st = st + 1 == DEC_STAGES ? 0 : st + 1;
         float4v sc = float4v{};
 #pragma unroll
@@ -380,7 +385,7 @@ __global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
             const half8 kop = *reinterpret_cast<const half8*>(sb + kaddr[s]);
             sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[s], sc, 0, 0, 0);
         }
-        const int t0 = t_lo + i * TT + 4 * grp;  // token of register 0
+        const int t0 = t_lo + (wave + NWV * i) * TT + 4 * grp;  // token of register 0
         float x[4], mb = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -418,24 +423,65 @@ __global__ __launch_bounds__(64) void decode_tiles(DecArgs a) {
     // Lane l holds head l%16, d = 16 dt + 4 (l/16) + r.
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
-    if (col >= QPG) return;
-    if (nact == 1) {
-        u16* o = a.O + ((long)b * a.H + g * QPG + col) * D + 4 * grp;
+    if constexpr (NWV == 1) {
+        if (col >= QPG) return;
+        if (nact == 1) {
+            u16* o = a.O + ((long)b * a.H + g * QPG + col) * D + 4 * grp;
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++) {
-            const uint32_t w0 = (uint32_t)f2h(acc[dt][0] / lsum) | ((uint32_t)f2h(acc[dt][1] / lsum) << 16);
-            const uint32_t w1 = (uint32_t)f2h(acc[dt][2] / lsum) | ((uint32_t)f2h(acc[dt][3] / lsum) << 16);
-            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-            *reinterpret_cast<u32x2_t*>(o + 16 * dt) = u32x2_t{w0, w1};
+            for (int dt = 0; dt < D / 16; dt++) {
+                const uint32_t w0 = (uint32_t)f2h(acc[dt][0] / lsum) | ((uint32_t)f2h(acc[dt][1] / lsum) << 16);
+                const uint32_t w1 = (uint32_t)f2h(acc[dt][2] / lsum) | ((uint32_t)f2h(acc[dt][3] / lsum) << 16);
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<u32x2_t*>(o + 16 * dt) = u32x2_t{w0, w1};
+            }
+        } else {
+            float* pe = a.part + ((((long)b * a.G + g) * a.NCH + c) * QPG + col) * (2 + D);
+            if (grp == 0) {
+                pe[0] = m;
+                pe[1] = lsum;
+            }
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++) *reinterpret_cast<float4v*>(pe + 2 + 16 * dt + 4 * grp) = acc[dt];
         }
     } else {
-        float* pe = a.part + ((((long)b * a.G + g) * a.NCH + c) * QPG + col) * (2 + D);
-        if (grp == 0) {
-            pe[0] = m;
-            pe[1] = lsum;
-        }
+        // Merge the wavefronts' states in LDS (the rings are idle), in wave order.
+        static_assert(NWV * QPG * (2 + D) * 4 <= NWV * DEC_STAGES * WSTAGE, "merge area exceeds the rings");
+        float* red = reinterpret_cast<float*>(lds);  // [NWV][QPG][2 + D]
+        __syncthreads();
+        if (col < QPG) {
+            float* rw = red + (wave * QPG + col) * (2 + D);
+            if (grp == 0) {
+                rw[0] = m;
+                rw[1] = lsum;
+            }
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++) *reinterpret_cast<float4v*>(pe + 2 + 16 * dt + 4 * grp) = acc[dt];
+            for (int dt = 0; dt < D / 16; dt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) rw[2 + 16 * dt + 4 * grp + r] = acc[dt][r];
+        }
+        __syncthreads();
+        for (int x = tid; x < QPG * D; x += 64 * NWV) {
+            const int i = x / D, d = x % D;
+            float M = red[i * (2 + D)];
+            for (int w = 1; w < NWV; w++) M = fmaxf(M, red[(w * QPG + i) * (2 + D)]);
+            float L = 0.0f, A = 0.0f;
+            for (int w = 0; w < NWV; w++) {
+                const float* rw = red + (w * QPG + i) * (2 + D);
+                const float f = __builtin_amdgcn_exp2f(rw[0] - M);
+                L += rw[1] * f;
+                A += rw[2 + d] * f;
+            }
+            if (nact == 1) {
+                a.O[((long)b * a.H + g * QPG + i) * D + d] = f2h(A / L);
+            } else {
+                float* pe = a.part + ((((long)b * a.G + g) * a.NCH + c) * QPG + i) * (2 + D);
+                if (d == 0) {
+                    pe[0] = M;
+                    pe[1] = L;
+                }
+                pe[2 + d] = A;
+            }
+        }
     }
 }
 
@@ -485,7 +531,11 @@ __global__ __launch_bounds__(256) void decode_merge(DecArgs a) {
 
 template <int D, int QPG>
 int run_decode_tiles(DecArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((decode_tiles<D, QPG>), dim3(a.B * a.G * a.NCH), dim3(64), 0, s, a);
+    constexpr int WIDE = D == 64 ? 8 : 4;  // wavefronts per workgroup of a one-chunk table (rings fit LDS)
+    if (a.NCH == 1)
+        hipLaunchKernelGGL((decode_tiles<D, QPG, WIDE>), dim3(a.B * a.G), dim3(64 * WIDE), 0, s, a);
+    else
+        hipLaunchKernelGGL((decode_tiles<D, QPG, 1>), dim3(a.B * a.G * a.NCH), dim3(64), 0, s, a);
     int r = TSL_LAUNCHED("decode_attention");
     if (r || a.NCH == 1) return r;
     const size_t lds = (size_t)a.NCH * QPG * (2 + D) * sizeof(float);
@@ -541,6 +591,9 @@ int chunk_pages(const TslKernel& k) {
     const int64_t bg = std::max<int64_t>(1, k.dim("B") * G), mp = k.dim("MP");
     const int64_t state = (H / std::max<int64_t>(1, G)) * (2 + k.dim("D")) * 4;  // bytes per chunk
     const int64_t ch = std::max((mp * bg + 2047) / 2048, (mp * state + 65535) / 65536);
+    // Short tables on the matrix-core path: one chunk, read by a workgroup of
+    // several wavefronts that merge in LDS (no second kernel).
+    if (tiles_path(k.dim("D"), k.dim("P")) && mp <= DEC_WIDE_MAX_PAGES) return (int)std::max<int64_t>(1, mp);
     return (int)std::min<int64_t>(DEC_MAX_CHUNK, std::max<int64_t>(2, ch));
 }
 int nchunks(const TslKernel& k) {
