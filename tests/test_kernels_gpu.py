@@ -395,3 +395,47 @@ def test_rope_and_kv_write(cfgname):
     parity("kv_write Kc", out[5], wKc)
     untouched = [i for i in range(NS) if i not in set(slot[:Tn - 2].tolist())]
     np.testing.assert_array_equal(out[5][untouched], Kc[untouched])
+
+
+# ---------------------------------------------------------------- graph replay
+
+def test_graph_replay_of_kernels_with_scratch():
+    # Handles that own scratch (split-K projection partials, chunked decode
+    # states) recorded into one graph and replayed several times, with eager
+    # work on the stream between replays: every replay matches the eager run.
+    _say("graph replay")
+    T.open()
+    r = oracle.Rng(21)
+    x = r.tensor("f16", [32, 5632], 1.0)
+    w = r.tensor("f16", [2048, 5632], 1.0 / np.sqrt(5632))
+    lin = T.kernel("llm", "linear", [[32, 5632], [2048, 5632], [32, 2048]])
+    q, kc, vc, table, lens, scale = decode_case(6, b=16, h=32, g=8, d=128, p=16, lo=1000, hi=4096)
+    dec = T.kernel("llm", "decode_attention", [list(q.shape), list(kc.shape), list(vc.shape), list(table.shape),
+                                               list(lens.shape), list(q.shape)])
+    lb = [T.tensor(x), T.tensor(w), T.alloc(32 * 2048 * 2)]
+    db = [T.tensor(a) for a in (q, kc, vc, table, lens)] + [T.alloc(q.nbytes), T.F32(scale)]
+    T.launch(lin, lb)
+    T.launch(dec, db)
+    T.sync()
+    want_l = T.read_array(lb[2], np.float16, (32, 2048))
+    want_d = T.read_array(db[5], np.float16, q.shape)
+    parity("graph linear eager", want_l, oracle.llm_linear(x, w))
+    parity("graph decode eager", want_d, oracle.decode_attention(q, kc, vc, table, lens, scale, threads=8))
+    T.capture_begin()
+    T.launch(lin, lb)
+    T.launch(dec, db)
+    g = T.capture_end()
+    other = T.kernel("llm", "linear", [[32, 5632], [2048, 5632], [32, 2048]])
+    ob = [T.tensor(x[::-1].copy()), lb[1], T.alloc(32 * 2048 * 2)]
+    for i in range(3):
+        for buf in (lb[2], db[5]):
+            T.fill_nan(buf)  # replays must rewrite the outputs
+        T.replay(g)
+        T.launch(other, ob)  # eager work between replays, on the same handle type
+        T.sync()
+        np.testing.assert_array_equal(T.read_array(lb[2], np.float16, (32, 2048)).view(np.uint16),
+                                      want_l.view(np.uint16))
+        np.testing.assert_array_equal(T.read_array(db[5], np.float16, q.shape).view(np.uint16),
+                                      want_d.view(np.uint16))
+    for b in lb + db[:6] + [ob[0], ob[2]]:
+        T.free(b)
