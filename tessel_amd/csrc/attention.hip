@@ -21,7 +21,6 @@
 
 namespace {
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int BQ = 128;  // queries per workgroup
 constexpr int BKEY = 64;  // keys per block

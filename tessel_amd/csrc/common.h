@@ -53,14 +53,6 @@ TSL_DEV float dpp(float x) {
 #define DPP_XOR2 0x4e
 #define DPP_HALF_MIRROR 0x141
 #define DPP_MIRROR 0x140
-// Sum over the 16 lanes of each row, every lane of the row receiving it.
-TSL_DEV float row16_sum(float x) {
-    x += dpp<DPP_XOR1>(x);
-    x += dpp<DPP_XOR2>(x);
-    x += dpp<DPP_HALF_MIRROR>(x);
-    x += dpp<DPP_MIRROR>(x);
-    return x;
-}
 
 // A kernel specialised by tsl_kernel: its resolved dimensions and meta
 // values, in the order the .tl signature names them.
@@ -72,7 +64,8 @@ struct TslKernel {
     int warps = 4;
     int nparams = 0;
     // Library-owned device scratch (allocated once per handle, outside any
-    // graph capture), e.g. split-context partials of decode attention.
+    // graph capture): decode attention's per-chunk states, the split-K
+    // partials of few-row projections.
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
     int64_t dim(const char* n) const;
