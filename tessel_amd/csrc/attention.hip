@@ -314,6 +314,11 @@ int prepare_attention(TslKernel& k) {
         return tsl_fail(-2, k.name + ": head dimension " + std::to_string(D) + " unsupported (16, 32, 64 or 128)");
     if (k.name == "prefill_attention" && k.dim("H") % k.dim("G") != 0)
         return tsl_fail(-2, "prefill_attention: H must be a multiple of G");
+    // K and V are read through 32-bit buffer ranges: a head's rows must span
+    // less than 4 GiB.
+    const int64_t row = k.name == "prefill_attention" ? k.dim("G") * D : D;
+    if (k.dim("S") * row * 2 >= (int64_t(1) << 32))
+        return tsl_fail(-2, k.name + ": K/V rows span 4 GiB or more (S x row too large)");
     return 0;
 }
 
