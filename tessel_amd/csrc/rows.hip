@@ -227,64 +227,73 @@ __global__ __launch_bounds__(256) void embed_kernel(const int* __restrict__ tok,
 // ---------------------------------------------------------------- rotary
 // rope_q: Q[t, h, i] = x1 c - x2 s and Q[t, h, D2 + i] = x2 c + x1 s with
 // x1 = QKV[t, h D + i], x2 = QKV[t, h D + D2 + i], (c, s) at pos[t].
-__global__ __launch_bounds__(256) void rope_q_kernel(const u16* __restrict__ QKV, const int* __restrict__ pos,
-                                                     const float* __restrict__ Cs, const float* __restrict__ Sn,
-                                                     u16* __restrict__ Q, int T, int W, int NPOS, int D2, int H,
-                                                     int D) {
-    const long n = (long)T * H * D2;
-    for (long e = (long)blockIdx.x * 256 + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
-        const int i = e % D2, h = (e / D2) % H, t = e / ((long)D2 * H);
-        const int p = pos[t];
-        const bool pin = p >= 0 && p < NPOS;
-        const float c = pin ? Cs[(size_t)p * D2 + i] : 0.0f, s = pin ? Sn[(size_t)p * D2 + i] : 0.0f;
-        const int c1 = h * D + i, c2 = h * D + D2 + i;
-        const float x1 = c1 < W ? h2f(QKV[(size_t)t * W + c1]) : 0.0f;
-        const float x2 = c2 < W ? h2f(QKV[(size_t)t * W + c2]) : 0.0f;
-        u16* q = Q + ((size_t)t * H + h) * D;
-        if (i < D) q[i] = f2h(x1 * c - x2 * s);
-        if (D2 + i < D) q[D2 + i] = f2h(x2 * c + x1 * s);
-    }
+struct RopeArgs {
+    const u16* QKV;
+    const int *pos, *slot;
+    const float *Cs, *Sn;
+    u16* Q;
+    u16 *Kc, *Vc, *K, *V;
+    int T, W, NPOS, D2, H, NS, G, D;
+};
+
+// Element e of rope_q's T x H x D2 index space.
+TSL_DEV void rope_q_elem(const RopeArgs& a, long e) {
+    const int i = e % a.D2, h = (e / a.D2) % a.H, t = e / ((long)a.D2 * a.H);
+    const int p = a.pos[t];
+    const bool pin = p >= 0 && p < a.NPOS;
+    const float c = pin ? a.Cs[(size_t)p * a.D2 + i] : 0.0f, s = pin ? a.Sn[(size_t)p * a.D2 + i] : 0.0f;
+    const int c1 = h * a.D + i, c2 = h * a.D + a.D2 + i;
+    const float x1 = c1 < a.W ? h2f(a.QKV[(size_t)t * a.W + c1]) : 0.0f;
+    const float x2 = c2 < a.W ? h2f(a.QKV[(size_t)t * a.W + c2]) : 0.0f;
+    u16* q = a.Q + ((size_t)t * a.H + h) * a.D;
+    if (i < a.D) q[i] = f2h(x1 * c - x2 * s);
+    if (a.D2 + i < a.D) q[a.D2 + i] = f2h(x2 * c + x1 * s);
 }
 
 // kv_write: the rotated keys and the values of kv head g into the paged
 // cache at slot[t] (dropped when outside [0, NS)) and into K, V [T, G, D].
-__global__ __launch_bounds__(256) void kv_write_kernel(const u16* __restrict__ QKV, const int* __restrict__ pos,
-                                                       const int* __restrict__ slot, const float* __restrict__ Cs,
-                                                       const float* __restrict__ Sn, u16* __restrict__ Kc,
-                                                       u16* __restrict__ Vc, u16* __restrict__ K, u16* __restrict__ V,
-                                                       int T, int W, int NPOS, int D2, int NS, int G, int D) {
-    const int nd = D2 > D ? D2 : D;
-    const long n = (long)T * G * nd;
+// Element e of its T x G x max(D2, D) index space.
+TSL_DEV void kv_write_elem(const RopeArgs& a, long e) {
+    const int nd = a.D2 > a.D ? a.D2 : a.D;
+    const int i = e % nd, g = (e / nd) % a.G, t = e / ((long)nd * a.G);
+    const int p = a.pos[t], at = a.slot[t];
+    const bool pin = p >= 0 && p < a.NPOS, ain = at >= 0 && at < a.NS;
+    const long k0 = (long)a.W - 2L * a.G * a.D + (long)g * a.D;
+    u16* kc = a.Kc + ((size_t)(ain ? at : 0) * a.G + g) * a.D;
+    u16* vc = a.Vc + ((size_t)(ain ? at : 0) * a.G + g) * a.D;
+    u16* kk = a.K + ((size_t)t * a.G + g) * a.D;
+    u16* vv = a.V + ((size_t)t * a.G + g) * a.D;
+    if (i < a.D2) {
+        const float c = pin ? a.Cs[(size_t)p * a.D2 + i] : 0.0f, s = pin ? a.Sn[(size_t)p * a.D2 + i] : 0.0f;
+        const long c1 = k0 + i, c2 = k0 + a.D2 + i;
+        const float x1 = (c1 >= 0 && c1 < a.W) ? h2f(a.QKV[(size_t)t * a.W + c1]) : 0.0f;
+        const float x2 = (c2 >= 0 && c2 < a.W) ? h2f(a.QKV[(size_t)t * a.W + c2]) : 0.0f;
+        const u16 y1 = f2h(x1 * c - x2 * s), y2 = f2h(x2 * c + x1 * s);
+        if (i < a.D) {
+            if (ain) kc[i] = y1;
+            kk[i] = y1;
+        }
+        if (a.D2 + i < a.D) {
+            if (ain) kc[a.D2 + i] = y2;
+            kk[a.D2 + i] = y2;
+        }
+    }
+    if (i < a.D) {
+        const long cv = k0 + (long)a.G * a.D + i;
+        const u16 v = (cv >= 0 && cv < a.W) ? a.QKV[(size_t)t * a.W + cv] : (u16)0;
+        if (ain) vc[i] = v;
+        vv[i] = v;
+    }
+}
+
+// KIND 0: rope_q, 1: kv_write, 2: both (the engine's fused step; the index
+// space of rope_q first, then kv_write's).
+template <int KIND>
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a, long nq, long nkv) {
+    const long n = nq + nkv;
     for (long e = (long)blockIdx.x * 256 + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
-        const int i = e % nd, g = (e / nd) % G, t = e / ((long)nd * G);
-        const int p = pos[t], at = slot[t];
-        const bool pin = p >= 0 && p < NPOS, ain = at >= 0 && at < NS;
-        const long k0 = (long)W - 2L * G * D + (long)g * D;
-        u16* kc = Kc + ((size_t)(ain ? at : 0) * G + g) * D;
-        u16* vc = Vc + ((size_t)(ain ? at : 0) * G + g) * D;
-        u16* kk = K + ((size_t)t * G + g) * D;
-        u16* vv = V + ((size_t)t * G + g) * D;
-        if (i < D2) {
-            const float c = pin ? Cs[(size_t)p * D2 + i] : 0.0f, s = pin ? Sn[(size_t)p * D2 + i] : 0.0f;
-            const long c1 = k0 + i, c2 = k0 + D2 + i;
-            const float x1 = (c1 >= 0 && c1 < W) ? h2f(QKV[(size_t)t * W + c1]) : 0.0f;
-            const float x2 = (c2 >= 0 && c2 < W) ? h2f(QKV[(size_t)t * W + c2]) : 0.0f;
-            const u16 y1 = f2h(x1 * c - x2 * s), y2 = f2h(x2 * c + x1 * s);
-            if (i < D) {
-                if (ain) kc[i] = y1;
-                kk[i] = y1;
-            }
-            if (D2 + i < D) {
-                if (ain) kc[D2 + i] = y2;
-                kk[D2 + i] = y2;
-            }
-        }
-        if (i < D) {
-            const long cv = k0 + (long)G * D + i;
-            const u16 v = (cv >= 0 && cv < W) ? QKV[(size_t)t * W + cv] : (u16)0;
-            if (ain) vc[i] = v;
-            vv[i] = v;
-        }
+        if (KIND == 0 || (KIND == 2 && e < nq)) rope_q_elem(a, e);
+        else kv_write_elem(a, e - nq);
     }
 }
 
@@ -351,21 +360,38 @@ int launch_rmsnorm_rows(TslKernel& k, const uint64_t* a, hipStream_t s) {
 }
 
 int launch_rope_q(TslKernel& k, const uint64_t* a, hipStream_t s) {
-    int T = k.dim("T"), W = k.dim("W"), NPOS = k.dim("NPOS"), D2 = k.dim("D2"), H = k.dim("H"), D = k.dim("D");
-    long n = (long)T * H * D2;
-    if (n == 0) return 0;
-    hipLaunchKernelGGL(rope_q_kernel, dim3(grid1(n)), dim3(256), 0, s, P<u16>(a[0]), P<int>(a[1]), P<float>(a[2]),
-                       P<float>(a[3]), P<u16>(a[4]), T, W, NPOS, D2, H, D);
+    RopeArgs r{};
+    r.T = k.dim("T"), r.W = k.dim("W"), r.NPOS = k.dim("NPOS"), r.D2 = k.dim("D2"), r.H = k.dim("H"), r.D = k.dim("D");
+    r.QKV = P<u16>(a[0]), r.pos = P<int>(a[1]), r.Cs = P<float>(a[2]), r.Sn = P<float>(a[3]), r.Q = P<u16>(a[4]);
+    const long nq = (long)r.T * r.H * r.D2;
+    if (nq == 0) return 0;
+    hipLaunchKernelGGL(rope_kernel<0>, dim3(grid1(nq)), dim3(256), 0, s, r, nq, 0L);
     return TSL_LAUNCHED("rope_q");
 }
 
 int launch_kv_write(TslKernel& k, const uint64_t* a, hipStream_t s) {
-    int T = k.dim("T"), W = k.dim("W"), NPOS = k.dim("NPOS"), D2 = k.dim("D2"), NS = k.dim("NS"), G = k.dim("G"),
-        D = k.dim("D");
-    long n = (long)T * G * std::max(D2, D);
-    if (n == 0) return 0;
-    hipLaunchKernelGGL(kv_write_kernel, dim3(grid1(n)), dim3(256), 0, s, P<u16>(a[0]), P<int>(a[1]), P<int>(a[2]),
-                       P<float>(a[3]), P<float>(a[4]), P<u16>(a[5]), P<u16>(a[6]), P<u16>(a[7]), P<u16>(a[8]), T, W,
-                       NPOS, D2, NS, G, D);
+    RopeArgs r{};
+    r.T = k.dim("T"), r.W = k.dim("W"), r.NPOS = k.dim("NPOS"), r.D2 = k.dim("D2"), r.NS = k.dim("NS");
+    r.G = k.dim("G"), r.D = k.dim("D");
+    r.QKV = P<u16>(a[0]), r.pos = P<int>(a[1]), r.slot = P<int>(a[2]), r.Cs = P<float>(a[3]), r.Sn = P<float>(a[4]);
+    r.Kc = P<u16>(a[5]), r.Vc = P<u16>(a[6]), r.K = P<u16>(a[7]), r.V = P<u16>(a[8]);
+    const long nkv = (long)r.T * r.G * std::max(r.D2, r.D);
+    if (nkv == 0) return 0;
+    hipLaunchKernelGGL(rope_kernel<1>, dim3(grid1(nkv)), dim3(256), 0, s, r, 0L, nkv);
     return TSL_LAUNCHED("kv_write");
+}
+
+// fused/rope_kv: rope_q and kv_write of the same step in one launch (the
+// engine's decode and prefill steps; not a .tl kernel). Arguments: QKV, pos,
+// slot, C, S, Q, Kc, Vc, K, V.
+int launch_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    RopeArgs r{};
+    r.T = k.dim("T"), r.W = k.dim("W"), r.NPOS = k.dim("NPOS"), r.D2 = k.dim("D2"), r.H = k.dim("H");
+    r.NS = k.dim("NS"), r.G = k.dim("G"), r.D = k.dim("D");
+    r.QKV = P<u16>(a[0]), r.pos = P<int>(a[1]), r.slot = P<int>(a[2]), r.Cs = P<float>(a[3]), r.Sn = P<float>(a[4]);
+    r.Q = P<u16>(a[5]), r.Kc = P<u16>(a[6]), r.Vc = P<u16>(a[7]), r.K = P<u16>(a[8]), r.V = P<u16>(a[9]);
+    const long nq = (long)r.T * r.H * r.D2, nkv = (long)r.T * r.G * std::max(r.D2, r.D);
+    if (nq + nkv == 0) return 0;
+    hipLaunchKernelGGL(rope_kernel<2>, dim3(grid1(nq + nkv)), dim3(256), 0, s, r, nq, nkv);
+    return TSL_LAUNCHED("rope_kv");
 }

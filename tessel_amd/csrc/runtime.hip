@@ -40,6 +40,7 @@ int launch_llm_rmsnorm(TslKernel&, const uint64_t*, hipStream_t);
 int launch_rmsnorm_rows(TslKernel&, const uint64_t*, hipStream_t);
 int launch_rope_q(TslKernel&, const uint64_t*, hipStream_t);
 int launch_kv_write(TslKernel&, const uint64_t*, hipStream_t);
+int launch_rope_kv(TslKernel&, const uint64_t*, hipStream_t);
 int launch_flash_attention(TslKernel&, const uint64_t*, hipStream_t);
 int launch_prefill_attention(TslKernel&, const uint64_t*, hipStream_t);
 int launch_decode_attention(TslKernel&, const uint64_t*, hipStream_t);
@@ -108,6 +109,12 @@ std::vector<KernelDef> g_defs = {
      "QKV: f16[T, W], pos: i32[T], slot: i32[T], C: f32[NPOS, D2], S: f32[NPOS, D2], Kc: f16[NS, G, D], "
      "Vc: f16[NS, G, D], K: f16[T, G, D], V: f16[T, G, D]",
      "", "D2 D", launch_kv_write, nullptr},
+    // Not a .tl kernel: llm/rope_q and llm/kv_write of one step in one launch
+    // (the engine's fusion; same arguments, Q after slot/C/S).
+    {"fused", "rope_kv",
+     "QKV: f16[T, W], pos: i32[T], slot: i32[T], C: f32[NPOS, D2], S: f32[NPOS, D2], Q: f16[T, H, D], "
+     "Kc: f16[NS, G, D], Vc: f16[NS, G, D], K: f16[T, G, D], V: f16[T, G, D]",
+     "", "D2 D", launch_rope_kv, nullptr},
     {"llm", "prefill_attention",
      "Q: f16[S, H, D], K: f16[S, G, D], V: f16[S, G, D], starts: i32[S], O: f16[S, H, D], scale: f32",
      "BM = 64, BN = 64", "D", launch_prefill_attention, prepare_attention},

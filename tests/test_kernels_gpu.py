@@ -395,6 +395,10 @@ def test_rope_and_kv_write(cfgname):
     parity("kv_write Kc", out[5], wKc)
     untouched = [i for i in range(NS) if i not in set(slot[:Tn - 2].tolist())]
     np.testing.assert_array_equal(out[5][untouched], Kc[untouched])
+    # The engine's fused launch (fused/rope_kv) writes exactly what the two do.
+    fz = T.run("fused", "rope_kv", [qkv, pos, slot, c, s, np.zeros((Tn, H, D), np.float16), Kc, Vc, K, V])
+    for got, ref in ((fz[5], q), (fz[6], out[5]), (fz[7], out[6]), (fz[8], out[7]), (fz[9], out[8])):
+        np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
 
 
 # ---------------------------------------------------------------- graph replay
