@@ -265,11 +265,16 @@ TSL_DEV half4 lds_read_tr(const u16* p) {
 // operand read cover all 16 slots of the 256-byte bank window); B row k (NN)
 // holds logical chunk c at c ^ ((k & 3) << 2), so the 4 k rows x 2 column
 // halves a 32-lane transposed read touches are 8 distinct 32-byte granules.
-template <bool BT, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS>
+//
+// With SPLIT, gridDim.y = S slices of K: workgroup (t, ks) runs the ks-th of S
+// slices of the K steps and leaves its f32 sums in part[ks][p][m][n] (p: gate,
+// up) for skinny_reduce, which adds the slices in order and applies the
+// epilogue.
+template <bool BT, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS, bool SPLIT = false>
 __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restrict__ A, const u16* __restrict__ B,
                                                              const u16* __restrict__ B2, void* __restrict__ C,
                                                              const u16* __restrict__ bias, int M, int N, int K,
-                                                             int G) {
+                                                             int G, float* __restrict__ part = nullptr) {
     constexpr int KC = BK / 8;                    // 16-byte chunks per LDS row of A (and W)
     static_assert((BK == 64 || BK == 32) && NS >= 2 && NS <= 4, "k step and stages");
     constexpr int NW = WGM * WGN;                 // wavefronts: WGM x WGN, each (BM/WGM) x (BN/WGN)
@@ -422,8 +427,9 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     // step kt (this wave's loads of later steps may still run), syncs (every
     // wave's loads have landed, and step kt-1's reads of its stage are done),
     // then refills that stage with step kt + NS - 1.
-    const int nk = (K + BK - 1) / BK;
-    for (int p = 0; p < NS - 1 && p < nk; p++) issue(p * BK, p);
+    const int nsteps = (K + BK - 1) / BK, S = SPLIT ? gridDim.y : 1, ks = SPLIT ? blockIdx.y : 0;
+    const int kbeg = (int)((long)ks * nsteps / S), nk = (int)((long)(ks + 1) * nsteps / S) - kbeg;
+    for (int p = 0; p < NS - 1 && p < nk; p++) issue((kbeg + p) * BK, p);
     half8 a0[TM], b0[TN], a1[TM], b1[TN], c0[DUAL ? TN : 1], c1[DUAL ? TN : 1];
     int stage = 0;
     for (int kt = 0; kt < nk; kt++) {
@@ -432,7 +438,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPS));
         else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LPS));
         __syncthreads();
-        if (kt + NS - 1 < nk) issue((kt + NS - 1) * BK, stage == 0 ? NS - 1 : stage - 1);
+        if (kt + NS - 1 < nk) issue((kbeg + kt + NS - 1) * BK, stage == 0 ? NS - 1 : stage - 1);
         const int so = stage * STAGE;
         stage = stage + 1 == NS ? 0 : stage + 1;
         read_ops(so, 0, a0, b0, c0);
@@ -477,19 +483,34 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         for (int j = 0; j < TN; j++) {
             const int col = n0 + wn0 + j * 32 + (lane & 31);
             if (col >= N) continue;
+            // The residual's 16 old values of this tile, all loads in flight
+            // before any store (the compiler cannot tell the stores from the
+            // loads apart, so an interleaved read-add-write runs serially).
+            float old[EPI == EPI_RESID && !SPLIT ? 16 : 1];
+            if constexpr (EPI == EPI_RESID && !SPLIT) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    old[r] = row < M ? reinterpret_cast<const float*>(C)[(size_t)row * N + col] : 0.0f;
+                }
+            }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
                 if (row >= M) continue;
                 const size_t o = (size_t)row * N + col;
                 const float v = acc[i][j][r];
-                if constexpr (EPI == EPI_F16) {
+                if constexpr (SPLIT) {
+                    const size_t mn = (size_t)M * N;
+                    float* pp = part + (size_t)ks * (DUAL ? 2 : 1) * mn + o;
+                    pp[0] = v;
+                    if constexpr (DUAL) pp[mn] = acc2[DUAL ? i : 0][DUAL ? j : 0][r];
+                } else if constexpr (EPI == EPI_F16) {
                     reinterpret_cast<u16*>(C)[o] = f2h(v);
                 } else if constexpr (EPI == EPI_F32) {
                     reinterpret_cast<float*>(C)[o] = v;
                 } else if constexpr (EPI == EPI_RESID) {
-                    float* R = reinterpret_cast<float*>(C);
-                    R[o] = R[o] + v;
+                    reinterpret_cast<float*>(C)[o] = old[r] + v;
                 } else if constexpr (EPI == EPI_BIAS) {
                     reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
                 } else {
@@ -698,6 +719,18 @@ SkPlan sk_plan(bool bt, int M, int N, int K) {
     return p;
 }
 
+// K slices for the 128 x 128 tiled path when its tiles alone leave CUs idle
+// (prefill-sized M): enough slices to give every CU a workgroup, each at
+// least 32 K steps long (shorter slices lose more to the extra partial
+// traffic and reduce launch than the idle CUs cost). 1 = no split.
+int big_split(int M, int N, int K) {
+    if (M <= 64 || K % 8) return 1;
+    const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
+    if (tiles >= 256 || tiles == 0) return 1;
+    const int nst = (K + 63) / 64;
+    return std::max(1, std::min((int)((256 + tiles - 1) / tiles), nst / 32));
+}
+
 template <int EPI, int MT, int RT>
 void launch_skinny_rt(const u16* X, const u16* W, const u16* W2, void* C, const u16* bias, int M, int N, int K,
                       int split, float* part, hipStream_t s) {
@@ -760,13 +793,32 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             return TSL_LAUNCHED(what);
         }
     }
+    if constexpr (DUAL) {
+        if (aligned && M > 64 && tiles(256, 128) >= 128) {
+            // 8 wavefronts of 64 x 64 x (gate, up): the 256 x 256 tile's
+            // register budget, and half the workgroups of 128 x 128 tiles, so
+            // prefill-sized products (M ~ 1024) fill the CUs in one round.
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 128, 4, 2, 64, 2>), dim3(tiles(256, 128)), dim3(512), 0, s, A, B, B2,
+                               C, bias, M, N, K, 4);
+            return TSL_LAUNCHED(what);
+        }
+    }
     if (aligned && M > 64 && (BT || !DUAL)) {
-        if (tiles(128, 128) >= 256) {
+        const int split = part ? big_split(M, N, K) : 1;
+        if (split > 1) {  // 128 x 128 tiles over K slices, then the ordered sum
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2, true>), dim3(tiles(128, 128), split), dim3(256), 0, s, A,
+                               B, B2, C, bias, M, N, K, 4, part);
+            const long mn = (long)M * N;
+            hipLaunchKernelGGL(skinny_reduce<EPI>, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, split, M,
+                               N, C, bias);
+        } else if (tiles(128, 128) >= 256) {
             hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
-        } else {  // 64 x 128 tiles (4 wavefronts of 64 x 32): twice the workgroups
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 128, 1, 4, 64, 2>), dim3(tiles(64, 128)), dim3(256), 0, s, A, B, B2, C,
-                               bias, M, N, K, 4);
+        } else {  // 64 x 128 tiles (4 wavefronts of 64 x 32): twice the workgroups;
+                  // X W^T keeps two K steps in flight (matmul's in-register B
+                  // transpose does better with one)
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 128, 1, 4, 64, BT ? 3 : 2>), dim3(tiles(64, 128)), dim3(256), 0, s, A,
+                               B, B2, C, bias, M, N, K, 4);
         }
         return TSL_LAUNCHED(what);
     }
@@ -828,15 +880,17 @@ int launch_gate_up(TslKernel& k, const uint64_t* a, hipStream_t s) {
                                            s, "gate_up", reinterpret_cast<float*>(k.scratch));
 }
 
-// Sizes the split-K partials of the skinny path (decode-sized M) once, when
-// the kernel is specialised: split x (2 for gate_up) x M x N floats.
+// Sizes the split-K partials (the skinny path at decode-sized M, the 128 x 128
+// path at prefill-sized M) once, when the kernel is specialised: split x (2
+// for gate_up) x M x N floats.
 int prepare_projection(TslKernel& k) {
     const bool dual = k.name == "gate_up";
     const int64_t M = k.dim("M"), N = dual ? k.dim("F") : k.dim("N"), K = k.dim("K");
     if (M > (1 << 20) || N > (1 << 30)) return 0;
     const SkPlan p = sk_plan(true, (int)M, (int)N, (int)K);
-    if (!p.use || p.split == 1) return 0;
-    const size_t bytes = (size_t)p.split * (dual ? 2 : 1) * M * N * sizeof(float);
+    const int split = p.use ? p.split : big_split((int)M, (int)N, (int)K);
+    if (split == 1) return 0;
+    const size_t bytes = (size_t)split * (dual ? 2 : 1) * M * N * sizeof(float);
     if (tsl_hip_check(hipMalloc(&k.scratch, bytes), "projection split-K scratch")) return -1;
     k.scratch_bytes = bytes;
     return 0;

@@ -114,7 +114,7 @@ def test_every_tuning_candidate(name, m):
         parity(f"{name} m={m} {meta}", got, want)
 
 
-@pytest.mark.parametrize("m", [1, 16, 32, 48, 64, 128, 512])
+@pytest.mark.parametrize("m", [1, 16, 32, 48, 64, 128, 512, 1024])
 @pytest.mark.parametrize("name", MM_CASES)
 def test_llm_matmuls_tinyllama_shapes(name, m):
     _say("llm mm", name, m)
@@ -138,6 +138,18 @@ def test_llm_matmuls_ragged_few_rows(name, m, k, n):
     parity(f"{name} {m}x{k}x{n}", got, want)
 
 
+@pytest.mark.parametrize("name", MM_CASES)
+@pytest.mark.parametrize("m,k,n", [(200, 4160, 300), (130, 4200, 260)])
+def test_llm_matmuls_ragged_split_tiles(name, m, k, n):
+    # Prefill-sized products whose 128 x 128 tiles are split over K (uneven
+    # slices, a partial last K step, ragged M and N).
+    _say("llm mm split tiles", name, m, k, n)
+    r = oracle.Rng(400 + m + n)
+    args, want = _mm_args(r, name, m, k, n, wscale=1.0 / np.sqrt(k))
+    got = T.run("llm", name, args, outputs=[len(args) - 1])[len(args) - 1]
+    parity(f"{name} {m}x{k}x{n}", got, want)
+
+
 def test_split_k_products_repeat_bit_identically():
     # The K-split partials are summed in slice order: repeated launches agree
     # bit for bit.
@@ -148,6 +160,11 @@ def test_split_k_products_repeat_bit_identically():
     for o in outs[1:]:
         np.testing.assert_array_equal(o.view(np.uint16), outs[0].view(np.uint16))
     parity("split-k linear", outs[0], want)
+    args, want = _mm_args(r, "linear_residual", 512, 5632, 2048, wscale=1.0 / np.sqrt(5632))
+    outs = [T.run("llm", "linear_residual", [a.copy() for a in args], outputs=[2])[2] for _ in range(3)]
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    parity("split-k tiles linear_residual", outs[0], want)
 
 
 # ---------------------------------------------------------------- attention
