@@ -294,7 +294,7 @@ struct Engine {
         std::memcpy(&eps_bits, &cfg.eps, 4);
         auto B = [](const Buf& b) { return Arg{Arg::BUF, b.p}; };
         Arg SC{Arg::F32, scale_bits}, EPS{Arg::F32, eps_bits};
-        int embed_k, norm_k, qkv_k, rope_k, att_k, oproj_k, gu_k, down_k;
+        int embed_k, norm_k, qkv_k, rope_k, att_k, gu_k, down_k;
         TRY(kernel("embed", {{T}, {vv, dm}, {T, dm}}, {{"BD", std::min<int64_t>(bc, 1024)}}, 4, &embed_k));
         TRY(kernel("rmsnorm", {{T, dm}, {dm}, {T, dm}}, {{"BC", bc}}, 4, &norm_k));
         const Layer& l0 = layers[0];
@@ -314,21 +314,32 @@ struct Engine {
                        {{T, nh, hd}, {lim.pages, p, ng, hd}, {lim.pages, p, ng, hd}, {T, mp}, {T}, {T, nh, hd}}, {}, 1,
                        &att_k));
         }
-        TRY(mm("linear_residual", {{T, nh * hd}, {dm, nh * hd}, {T, dm}}, false, {B(o), B(l0.wo), B(x)}, &oproj_k));
         TRY(mm("gate_up", {{T, dm}, {f, dm}, {f, dm}, {T, f}}, true, {B(h), B(l0.wg), B(l0.wu), B(mlp)}, &gu_k));
         TRY(mm("linear_residual", {{T, f}, {dm, f}, {T, dm}}, false, {B(mlp), B(l0.wd), B(x)}, &down_k));
+        // A residual projection and the rmsnorm that follows it, as one
+        // launch sequence (fused/linear_residual_rmsnorm): the o projection
+        // with mlp_norm, and the down projection with the next layer's
+        // attn_norm.
+        int oproj_norm_k, down_norm_k;
+        TRY(kernel("linear_residual_rmsnorm", {{T, nh * hd}, {dm, nh * hd}, {T, dm}, {dm}, {T, dm}}, {{"BC", bc}}, 4,
+                   &oproj_norm_k, "fused"));
+        TRY(kernel("linear_residual_rmsnorm", {{T, f}, {dm, f}, {T, dm}, {dm}, {T, dm}}, {{"BC", bc}}, 4,
+                   &down_norm_k, "fused"));
 
         TRY(launch(embed_k, {B(tok), B(embed), B(x)}));
-        for (auto& L : layers) {
-            TRY(launch(norm_k, {B(x), B(L.n1), B(h), EPS}));
+        TRY(launch(norm_k, {B(x), B(layers[0].n1), B(h), EPS}));
+        for (size_t li = 0; li < layers.size(); li++) {
+            const Layer& L = layers[li];
             TRY(launch(qkv_k, {B(h), B(L.wqkv), B(qkv)}));
             TRY(launch(rope_k, {B(qkv), B(pos), B(slot), B(cos), B(sin), B(q), B(L.kc), B(L.vc), B(k), B(v)}));
             if (prefill) TRY(launch(att_k, {B(q), B(k), B(v), B(starts), B(o), SC}));
             else TRY(launch(att_k, {B(q), B(L.kc), B(L.vc), B(table), B(lens), B(o), SC}));
-            TRY(launch(oproj_k, {B(o), B(L.wo), B(x)}));
-            TRY(launch(norm_k, {B(x), B(L.n2), B(h), EPS}));
+            TRY(launch(oproj_norm_k, {B(o), B(L.wo), B(x), B(L.n2), B(h), EPS}));
             TRY(launch(gu_k, {B(h), B(L.wg), B(L.wu), B(mlp)}));
-            TRY(launch(down_k, {B(mlp), B(L.wd), B(x)}));
+            if (li + 1 < layers.size())
+                TRY(launch(down_norm_k, {B(mlp), B(L.wd), B(x), B(layers[li + 1].n1), B(h), EPS}));
+            else
+                TRY(launch(down_k, {B(mlp), B(L.wd), B(x)}));
         }
         if (bw == 0) return 0;
         int fin_k, head_k;

@@ -16,6 +16,11 @@
 
 #include <algorithm>
 
+bool reduce_rmsnorm_fits(int C);
+int run_reduce_rmsnorm(const float* part, int S, float* R, const u16* W, u16* Y, int M, int C, float eps,
+                       hipStream_t s);
+int run_rmsnorm_f32(const float* X, const u16* W, u16* Y, int M, int C, int ncols, float eps, hipStream_t s);
+
 namespace {
 
 constexpr int NUM_XCD = 8;
@@ -731,13 +736,15 @@ int big_split(int M, int N, int K) {
     return std::max(1, std::min((int)((256 + tiles - 1) / tiles), nst / 32));
 }
 
+// reduce = false leaves a split product's slices in part (the caller sums them).
 template <int EPI, int MT, int RT>
 void launch_skinny_rt(const u16* X, const u16* W, const u16* W2, void* C, const u16* bias, int M, int N, int K,
-                      int split, float* part, hipStream_t s) {
+                      int split, float* part, hipStream_t s, bool reduce) {
     const unsigned blocks = (N + 16 * RT - 1) / (16 * RT);
     if (split > 1) {
         hipLaunchKernelGGL((gemm_skinny<EPI, MT, RT, true>), dim3(blocks, split), dim3(64 * SK_WAVES), 0, s, X, W, W2, C,
                            bias, M, N, K, part);
+        if (!reduce) return;
         const long mn = (long)M * N;
         hipLaunchKernelGGL(skinny_reduce<EPI>, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, split, M, N,
                            C, bias);
@@ -749,9 +756,20 @@ void launch_skinny_rt(const u16* X, const u16* W, const u16* W2, void* C, const 
 
 template <int EPI, int MT>
 void launch_skinny(const u16* X, const u16* W, const u16* W2, void* C, const u16* bias, int M, int N, int K,
-                   const SkPlan& p, float* part, hipStream_t s) {
-    if (p.rt == 2) launch_skinny_rt<EPI, MT, 2>(X, W, W2, C, bias, M, N, K, p.split, part, s);
-    else launch_skinny_rt<EPI, MT, 1>(X, W, W2, C, bias, M, N, K, p.split, part, s);
+                   const SkPlan& p, float* part, hipStream_t s, bool reduce = true) {
+    if (p.rt == 2) launch_skinny_rt<EPI, MT, 2>(X, W, W2, C, bias, M, N, K, p.split, part, s, reduce);
+    else launch_skinny_rt<EPI, MT, 1>(X, W, W2, C, bias, M, N, K, p.split, part, s, reduce);
+}
+
+template <int EPI>
+void launch_skinny_m(const u16* X, const u16* W, const u16* W2, void* C, const u16* bias, int M, int N, int K,
+                     const SkPlan& p, float* part, hipStream_t s, bool reduce = true) {
+    switch ((M + 15) / 16) {
+        case 1: launch_skinny<EPI, 1>(X, W, W2, C, bias, M, N, K, p, part, s, reduce); break;
+        case 2: launch_skinny<EPI, 2>(X, W, W2, C, bias, M, N, K, p, part, s, reduce); break;
+        case 3: launch_skinny<EPI, 3>(X, W, W2, C, bias, M, N, K, p, part, s, reduce); break;
+        default: launch_skinny<EPI, 4>(X, W, W2, C, bias, M, N, K, p, part, s, reduce); break;
+    }
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool BT, int EPI>
@@ -774,12 +792,7 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
     if constexpr (BT) {
         const SkPlan p = sk_plan(true, M, N, K);
         if (p.use && (p.split == 1 || part)) {  // a weight stream: the skinny path
-            switch ((M + 15) / 16) {
-                case 1: launch_skinny<EPI, 1>(A, B, B2, C, bias, M, N, K, p, part, s); break;
-                case 2: launch_skinny<EPI, 2>(A, B, B2, C, bias, M, N, K, p, part, s); break;
-                case 3: launch_skinny<EPI, 3>(A, B, B2, C, bias, M, N, K, p, part, s); break;
-                default: launch_skinny<EPI, 4>(A, B, B2, C, bias, M, N, K, p, part, s); break;
-            }
+            launch_skinny_m<EPI>(A, B, B2, C, bias, M, N, K, p, part, s);
             return TSL_LAUNCHED(what);
         }
     }
@@ -880,6 +893,37 @@ int launch_gate_up(TslKernel& k, const uint64_t* a, hipStream_t s) {
                                            s, "gate_up", reinterpret_cast<float*>(k.scratch));
 }
 
+// fused/linear_residual_rmsnorm (the engine's fusion, not a .tl kernel):
+// llm/linear_residual then llm/rmsnorm of the updated residual, arguments
+// X [M, K], W [N, K], R [M, N], Wn [N], Y [M, N], eps. Few-row products run
+// K-split (at least 2 slices) and one kernel adds the slices to R and
+// normalises each row; with the slice count linear_residual would use, the
+// bits are that pair's. Other shapes launch the pair.
+SkPlan fused_plan(int M, int N, int K, int ncols) {
+    SkPlan p = sk_plan(true, M, N, K);
+    if (!p.use || ncols != N || !reduce_rmsnorm_fits(N)) return SkPlan{};
+    if (p.split == 1 && K / 64 >= 2 * SK_WAVES) p.split = 2;
+    if (p.split == 1) return SkPlan{};
+    return p;
+}
+
+int launch_linear_residual_rmsnorm(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    const int M = k.dim("M"), N = k.dim("N"), K = k.dim("K");
+    const int ncols = (int)std::min<int64_t>(k.metav("BC"), N);
+    const float eps = arg_f32(a[5]);
+    float* R = P<float>(a[2]);
+    const SkPlan p = fused_plan(M, N, K, ncols);
+    if (p.use && k.scratch) {
+        float* part = reinterpret_cast<float*>(k.scratch);
+        launch_skinny_m<EPI_RESID>(P<u16>(a[0]), P<u16>(a[1]), nullptr, R, nullptr, M, N, K, p, part, s, false);
+        return run_reduce_rmsnorm(part, p.split, R, P<u16>(a[3]), P<u16>(a[4]), M, N, eps, s);
+    }
+    if (int e = gemm_dispatch<true, EPI_RESID>(P<u16>(a[0]), P<u16>(a[1]), nullptr, R, nullptr, M, N, K, s,
+                                               "linear_residual_rmsnorm", reinterpret_cast<float*>(k.scratch)))
+        return e;
+    return run_rmsnorm_f32(R, P<u16>(a[3]), P<u16>(a[4]), M, N, ncols, eps, s);
+}
+
 // Sizes the split-K partials (the skinny path at decode-sized M, the 128 x 128
 // path at prefill-sized M) once, when the kernel is specialised: split x (2
 // for gate_up) x M x N floats.
@@ -887,7 +931,11 @@ int prepare_projection(TslKernel& k) {
     const bool dual = k.name == "gate_up";
     const int64_t M = k.dim("M"), N = dual ? k.dim("F") : k.dim("N"), K = k.dim("K");
     if (M > (1 << 20) || N > (1 << 30)) return 0;
-    const SkPlan p = sk_plan(true, (int)M, (int)N, (int)K);
+    SkPlan p = sk_plan(true, (int)M, (int)N, (int)K);
+    if (k.name == "linear_residual_rmsnorm") {
+        const SkPlan f = fused_plan((int)M, (int)N, (int)K, (int)std::min<int64_t>(k.metav("BC"), N));
+        if (f.use) p = f;
+    }
     const int split = p.use ? p.split : big_split((int)M, (int)N, (int)K);
     if (split == 1) return 0;
     const size_t bytes = (size_t)split * (dual ? 2 : 1) * M * N * sizeof(float);

@@ -82,6 +82,35 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const float* __restri
 // y = x * (1 / sqrt(sum(x^2 over BC columns) / n + eps)) * w, over the
 // first ncols = min(BC, C) columns (columns past C read 0). XT is f16
 // (basic.tl) or f32 (llm.tl); `rows` (rmsnorm_rows) gathers the input row.
+// Writes y[c] = f16(v * rs * w[c]) for this lane's NV chunks of E columns
+// (chunk i starts at column (64 i + lane) E), the first ncols columns only.
+template <int E, int NV>
+TSL_DEV void rms_store(const float (&v)[NV][E], float rs, const u16* __restrict__ W, u16* __restrict__ y, int lane,
+                       int ncols, bool vec) {
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = (i * 64 + lane) * E;
+        if (vec && c + E <= ncols) {
+            // E outputs: 8 halves (16 bytes) for f16 input rows, 4 (8 bytes) for f32.
+            uint32_t o[E / 2];
+            for (int p = 0; p < E / 2; p++) {
+                u16 lo = f2h(v[i][2 * p] * rs * h2f(W[c + 2 * p]));
+                u16 hi = f2h(v[i][2 * p + 1] * rs * h2f(W[c + 2 * p + 1]));
+                o[p] = (uint32_t)lo | ((uint32_t)hi << 16);
+            }
+            if constexpr (E == 8) {
+                *reinterpret_cast<u32x4*>(y + c) = u32x4{o[0], o[1], o[2], o[3]};
+            } else {
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<u32x2*>(y + c) = u32x2{o[0], o[1]};
+            }
+        } else {
+            for (int e = 0; e < E; e++)
+                if (c + e < ncols) y[c + e] = f2h(v[i][e] * rs * h2f(W[c + e]));
+        }
+    }
+}
+
 template <typename XT, int NV>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ X, const int* __restrict__ idx,
                                                       int xrows, const u16* __restrict__ W, u16* __restrict__ Y,
@@ -122,28 +151,133 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ X, 
     }
     ss = wave_sum(ss);
     const float rs = 1.0f / sqrtf(ss / n + eps);
+    rms_store<E, NV>(v, rs, W, y, lane, ncols, vec);
+}
+
+// ---- one workgroup per row (llm.tl rmsnorm over f32 rows, and the fused
+// residual projection): thread t owns the float4 chunks t, t + 256, ... of
+// the row, so a decode-sized batch (a few dozen rows) still spreads its
+// loads over 256 lanes per row, all issued before the reduction.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Loads this thread's chunks of W (zeros past ncols).
+template <int NC>
+TSL_DEV void rms_wg_weights(const u16* __restrict__ W, int t, int ncols, u32x2 (&w)[NC]) {
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int c = (i * 64 + lane) * E;
-        if (vec && c + E <= ncols) {
-            // E outputs: 8 halves (16 bytes) for f16 input rows, 4 (8 bytes) for f32.
-            uint32_t o[E / 2];
-            for (int p = 0; p < E / 2; p++) {
-                u16 lo = f2h(v[i][2 * p] * rs * h2f(W[c + 2 * p]));
-                u16 hi = f2h(v[i][2 * p + 1] * rs * h2f(W[c + 2 * p + 1]));
-                o[p] = (uint32_t)lo | ((uint32_t)hi << 16);
-            }
-            if constexpr (E == 8) {
-                *reinterpret_cast<u32x4*>(y + c) = u32x4{o[0], o[1], o[2], o[3]};
-            } else {
-                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-                *reinterpret_cast<u32x2*>(y + c) = u32x2{o[0], o[1]};
-            }
+    for (int i = 0; i < NC; i++) {
+        const int c = (i * 256 + t) * 4;
+        if (c + 4 <= ncols) {
+            w[i] = *reinterpret_cast<const u32x2*>(W + c);
         } else {
-            for (int e = 0; e < E; e++)
-                if (c + e < ncols) y[c + e] = f2h(v[i][e] * rs * h2f(W[c + e]));
+            uint32_t h[4];
+            for (int e = 0; e < 4; e++) h[e] = c + e < ncols ? W[c + e] : 0;
+            w[i] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
         }
     }
+}
+
+// Given this thread's values v (zero past ncols) and weights, writes
+// y[c] = f16(v * rs * w[c]) for the first ncols columns, rs = 1 / sqrt(sum
+// of squares of the row / n + eps): per-thread sums in chunk order, then
+// the wavefront butterfly, then the 4 wavefronts in order.
+template <int NC>
+TSL_DEV void rms_wg_finish(const float4v (&v)[NC], const u32x2 (&w)[NC], int t, int ncols, float n, float eps,
+                           u16* __restrict__ y, float* red) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NC; i++)
+        for (int e = 0; e < 4; e++) ss += v[i][e] * v[i][e];
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const float rs = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / n + eps);
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const int c = (i * 256 + t) * 4;
+        u16 o[4];
+        for (int e = 0; e < 4; e++) o[e] = f2h(v[i][e] * rs * h2f((u16)(w[i][e >> 1] >> (16 * (e & 1)))));
+        if (c + 4 <= ncols) {
+            *reinterpret_cast<u32x2*>(y + c) = u32x2{o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16)};
+        } else {
+            for (int e = 0; e < 4; e++)
+                if (c + e < ncols) y[c + e] = o[e];
+        }
+    }
+}
+
+// llm.tl rmsnorm / rmsnorm_rows over f32 rows with C % 4 == 0 and
+// ncols <= 1024 NC; idx (rmsnorm_rows) gathers the input row.
+template <int NC>
+__global__ __launch_bounds__(256) void rmsnorm_wg_kernel(const float* __restrict__ X, const int* __restrict__ idx,
+                                                         int xrows, const u16* __restrict__ W, u16* __restrict__ Y,
+                                                         int C, int ncols, float n, float eps) {
+    __shared__ float red[4];
+    const int t = threadIdx.x, row = blockIdx.x;
+    const int src = idx ? idx[row] : row;
+    const bool rin = src >= 0 && src < xrows;
+    const float* x = X + (size_t)(rin ? src : 0) * C;
+    float4v v[NC];
+    u32x2 w[NC];
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const int c = (i * 256 + t) * 4;
+        if (rin && c + 4 <= ncols) {
+            v[i] = *reinterpret_cast<const float4v*>(x + c);
+        } else {
+            for (int e = 0; e < 4; e++) v[i][e] = rin && c + e < ncols ? x[c + e] : 0.0f;
+        }
+    }
+    rms_wg_weights<NC>(W, t, ncols, w);
+    rms_wg_finish<NC>(v, w, t, ncols, n, eps, Y + (size_t)row * C, red);
+}
+
+// The engine's fused step after a K-split residual projection: R[m] += the
+// S slices of part[ks][m], added in slice order as skinny_reduce adds them,
+// then Y[m] = rmsnorm(R[m]) W as rmsnorm_wg_kernel computes it, over all C
+// columns (C % 4 == 0, C <= 1024 NC): the bits of llm/linear_residual (same
+// split) followed by llm/rmsnorm. SU > 0: S == SU, every load of the row
+// issued at once; 0: any S.
+template <int NC, int SU>
+__global__ __launch_bounds__(256) void reduce_rmsnorm_kernel(const float* __restrict__ part, int S,
+                                                             float* __restrict__ R, const u16* __restrict__ W,
+                                                             u16* __restrict__ Y, int M, int C, float n, float eps) {
+    __shared__ float red[4];
+    const int t = threadIdx.x, row = blockIdx.x;
+    const size_t mc = (size_t)M * C;
+    float* r = R + (size_t)row * C;
+    const float* pr = part + (size_t)row * C;
+    const float4v z = {0.0f, 0.0f, 0.0f, 0.0f};
+    float4v old[NC], acc[NC];
+    u32x2 w[NC];
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const int c = (i * 256 + t) * 4;
+        old[i] = c < C ? *reinterpret_cast<const float4v*>(r + c) : z;
+        acc[i] = z;
+    }
+    rms_wg_weights<NC>(W, t, C, w);
+    auto slice = [&](int ks) {
+#pragma unroll
+        for (int i = 0; i < NC; i++) {
+            const int c = (i * 256 + t) * 4;
+            if (c < C) acc[i] += *reinterpret_cast<const float4v*>(pr + ks * mc + c);
+        }
+    };
+    if constexpr (SU > 0) {
+#pragma unroll
+        for (int ks = 0; ks < SU; ks++) slice(ks);
+    } else {
+        for (int ks = 0; ks < S; ks++) slice(ks);
+    }
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const int c = (i * 256 + t) * 4;
+        if (c < C) {
+            old[i] += acc[i];
+            *reinterpret_cast<float4v*>(r + c) = old[i];
+        }
+    }
+    rms_wg_finish<NC>(old, w, t, C, n, eps, Y + (size_t)row * C, red);
 }
 
 template <typename XT>
@@ -173,9 +307,20 @@ template <typename XT>
 int run_rmsnorm(const XT* X, const int* idx, int xrows, const u16* W, u16* Y, int R, int C, int ncols, float eps,
                 hipStream_t s, const char* what) {
     if (R == 0) return 0;
+    const float n = (float)C;
+    if constexpr (sizeof(XT) == 4) {
+        if (C % 4 == 0 && ncols <= 4096) {
+            if (ncols <= 1024)
+                hipLaunchKernelGGL(rmsnorm_wg_kernel<1>, dim3(R), dim3(256), 0, s, X, idx, xrows, W, Y, C, ncols, n, eps);
+            else if (ncols <= 2048)
+                hipLaunchKernelGGL(rmsnorm_wg_kernel<2>, dim3(R), dim3(256), 0, s, X, idx, xrows, W, Y, C, ncols, n, eps);
+            else
+                hipLaunchKernelGGL(rmsnorm_wg_kernel<4>, dim3(R), dim3(256), 0, s, X, idx, xrows, W, Y, C, ncols, n, eps);
+            return TSL_LAUNCHED(what);
+        }
+    }
     dim3 grid((R + ROWS_PER_WG - 1) / ROWS_PER_WG);
     constexpr int E = 16 / sizeof(XT);
-    const float n = (float)C;
     if (ncols <= 64 * E * 4)
         hipLaunchKernelGGL((rmsnorm_kernel<XT, 4>), grid, dim3(256), 0, s, X, idx, xrows, W, Y, R, C, ncols, n, eps);
     else if (ncols <= 64 * E * 8)
@@ -343,6 +488,35 @@ int launch_embed(TslKernel& k, const uint64_t* a, hipStream_t s) {
     dim3 grid((Dm + 2047) / 2048, T);
     hipLaunchKernelGGL(embed_kernel, grid, dim3(256), 0, s, P<int>(a[0]), P<u16>(a[1]), P<float>(a[2]), T, V, Dm);
     return TSL_LAUNCHED("embed");
+}
+
+// For the fused residual projection (gemm.hip): R += the S slices of part,
+// then Y = rmsnorm(R) W (C % 4 == 0, C <= 4096; reduce_rmsnorm_kernel).
+bool reduce_rmsnorm_fits(int C) { return C > 0 && C % 4 == 0 && C <= 4096; }
+int run_reduce_rmsnorm(const float* part, int S, float* R, const u16* W, u16* Y, int M, int C, float eps,
+                       hipStream_t s) {
+    if (M == 0) return 0;
+    auto go = [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+        auto k = [&](auto su) {
+            hipLaunchKernelGGL((reduce_rmsnorm_kernel<NC, decltype(su)::value>), dim3(M), dim3(256), 0, s, part, S, R,
+                               W, Y, M, C, (float)C, eps);
+        };
+        switch (S) {
+            case 2: k(std::integral_constant<int, 2>{}); break;
+            case 3: k(std::integral_constant<int, 3>{}); break;
+            case 4: k(std::integral_constant<int, 4>{}); break;
+            default: k(std::integral_constant<int, 0>{}); break;
+        }
+    };
+    if (C <= 1024) go(std::integral_constant<int, 1>{});
+    else if (C <= 2048) go(std::integral_constant<int, 2>{});
+    else go(std::integral_constant<int, 4>{});
+    return TSL_LAUNCHED("linear_residual_rmsnorm");
+}
+// llm/rmsnorm over f32 rows, for the fused projection's unsplit path.
+int run_rmsnorm_f32(const float* X, const u16* W, u16* Y, int M, int C, int ncols, float eps, hipStream_t s) {
+    return run_rmsnorm<float>(X, nullptr, M, W, Y, M, C, ncols, eps, s, "linear_residual_rmsnorm");
 }
 
 int launch_llm_rmsnorm(TslKernel& k, const uint64_t* a, hipStream_t s) {

@@ -384,6 +384,36 @@ def test_llm_rows(t, dm):
     np.testing.assert_array_equal(got, oracle.embed(tok, e))
 
 
+@pytest.mark.parametrize("m,k,n,mode", [(32, 5632, 2048, "split"), (32, 2048, 2048, "own split"),
+                                        (5, 1024, 1000, "own split"), (7, 4160, 33, "pair"), (128, 2048, 2048, "pair"),
+                                        (200, 4160, 300, "pair")])
+def test_fused_linear_residual_rmsnorm(m, k, n, mode):
+    # The engine's fused launch (fused/linear_residual_rmsnorm): R += X W^T,
+    # then Y = rmsnorm(R) Wn, against the oracle and against llm/linear_residual
+    # followed by llm/rmsnorm. "pair": the shape launches exactly that pair.
+    # "split": K is split as linear_residual splits it, so R and Y have the
+    # pair's bits too. "own split": a split linear_residual does not make, so
+    # R and Y are within the float tolerance.
+    _say("fused linear_residual_rmsnorm", m, k, n)
+    r = oracle.Rng(500 + m + n)
+    x = r.tensor("f16", [m, k], 1.0)
+    w = r.tensor("f16", [n, k], 1.0 / np.sqrt(k))
+    res = r.tensor("f32", [m, n], 1.0)
+    wn = r.tensor("f16", [n], 1.0)
+    bc = 1 << (n - 1).bit_length()
+    eps = [T.F32(1e-5)]
+    out = T.run("fused", "linear_residual_rmsnorm", [x, w, res.copy(), wn, np.zeros((m, n), np.float16)], eps,
+                meta=[("BC", bc)], outputs=[2, 4])
+    pr = T.run("llm", "linear_residual", [x, w, res.copy()], outputs=[2])[2]
+    py = T.run("llm", "rmsnorm", [pr, wn, np.zeros((m, n), np.float16)], eps, meta=[("BC", bc)], outputs=[2])[2]
+    want_r = oracle.linear_residual(x, w, res.copy())
+    parity("fused R", out[2], want_r)
+    parity("fused Y", out[4], oracle.rmsnorm(want_r.astype(np.float32), wn, 1e-5, BC=bc))
+    if mode in ("split", "pair"):
+        np.testing.assert_array_equal(out[2].view(np.uint32), pr.view(np.uint32))
+        np.testing.assert_array_equal(out[4].view(np.uint16), py.view(np.uint16))
+
+
 @pytest.mark.parametrize("cfgname", ["tiny", "tinyllama"])
 def test_rope_and_kv_write(cfgname):
     _say("rope/kv_write", cfgname)
