@@ -564,7 +564,9 @@ __global__ __launch_bounds__(256) void matmul_f32_kernel(const float* __restrict
 // runs on v_mfma_f32_16x16x32_f16, one 16-row tile of X per MT. The 8
 // partial tiles are summed in LDS in wavefront order (deterministic), then
 // the epilogue writes Y. Needs K % 64 == 0; rows past M or N read as zero and
-// their outputs are dropped.
+// their outputs are dropped. This register-operand form serves K % 128 != 0;
+// otherwise gemm_skinny_lds (below) stages both operands in LDS with whole
+// 128-byte lines per load, which streams W about 1.5x faster.
 constexpr int SK_WAVES = 8;
 
 // The epilogue of one output (m, n): v = (X W^T)[m, n], u its SwiGLU partner.
@@ -692,6 +694,167 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const u16* __restri
         }
 }
 
+// The skinny product with both operands staged in LDS (K % 128 == 0). A
+// workgroup owns a block of 16 rows of W (gate_up: 8 rows of Wg and the same
+// 8 rows of Wu) over a slice of at most SL_KS k values:
+// - W: at the start, every load of the block at once, as direct-to-LDS
+//   loads of 1 KB runs of a row's slice (whole 128-byte lines, in address
+//   order). Chunk c (16 bytes) of row r sits at position c ^ (r & 15) of its
+//   LDS row, so the 16 rows an operand read touches fall in distinct bank
+//   groups.
+// - X: each wavefront takes interleaved 64-wide k steps and loads a step's
+//   X rows (16 MT x 128 bytes, 8 whole lines per load) into its own LDS ring
+//   of XD stages, chunk c of row r at position c ^ ((r >> 1) & 7).
+// Y^T (16 n x 16 m) += W (16 n x 32 k) X^T (32 k x 16 m) on
+// v_mfma_f32_16x16x32_f16; the 8 partial tiles are summed in LDS in
+// wavefront order, then the epilogue (or the split layout of gemm_skinny).
+constexpr int SL_KS = 2048;
+template <int MT>
+constexpr int sl_xdepth() { return MT <= 2 ? 2 : 1; }
+template <int EPI, int MT, bool SPLIT>
+__global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __restrict__ X, const u16* __restrict__ W,
+                                                                   const u16* __restrict__ W2, void* C,
+                                                                   const u16* __restrict__ bias, int M, int N, int K,
+                                                                   float* __restrict__ part) {
+    constexpr bool DUAL = EPI == EPI_SWIGLU;
+    constexpr int WB = 16 * SL_KS * 2;           // LDS bytes of the W block
+    constexpr int XS = 16 * MT * 128;            // LDS bytes of one X step
+    constexpr int XD = sl_xdepth<MT>();          // X stages per wavefront
+    constexpr int MAXU = SL_KS / 64 / SK_WAVES;  // k steps per wavefront
+    constexpr int XL = 2 * MT;                   // X loads per step (8 rows each)
+    __shared__ __attribute__((aligned(16))) u16 lds[(WB + SK_WAVES * XD * XS) / 2];
+    __shared__ float red[SK_WAVES][4][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row = lane & 15, g = lane >> 4;
+    // Rows of this block: n0 .. n0 + 15 of W, or n0 .. n0 + 7 of Wg and of Wu.
+    const int n0 = blockIdx.x * (DUAL ? 8 : 16);
+    const int nb = K / 128, S = SPLIT ? gridDim.y : 1, ks = SPLIT ? blockIdx.y : 0;
+    const int b0 = ks * nb / S, b1 = (ks + 1) * nb / S;
+    const int k0 = 128 * b0, KS = 128 * (b1 - b0), cpr = KS / 8, nst = KS / 64;
+    const uint32_t lds_w = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
+    const uint32_t lds_x = lds_w + WB + wave * XD * XS;
+
+    // W block: 16 cpr chunks; load q covers linear chunks 64 q .. 64 q + 63
+    // (row p / cpr, position p % cpr). Rows past N read as zero.
+    {
+        const int rows = min(DUAL ? 8 : 16, N - n0);
+        const uint32_t range = (uint32_t)(((long)(rows - 1) * K + KS) * 2);
+        const i32x4 rw = make_rsrc(W + (size_t)n0 * K + k0, range);
+        const i32x4 rw2 = make_rsrc((DUAL ? W2 : W) + (size_t)n0 * K + k0, range);
+        const int nq = cpr / 4;
+        for (int q = wave; q < nq; q += SK_WAVES) {
+            const int p = 64 * q + lane, r = p / cpr, pos = p - r * cpr;
+            const int rr = DUAL ? r & 7 : r;  // row within its matrix
+            const uint32_t off = (uint32_t)((rr * K + 8 * (pos ^ (r & 15))) * 2);
+            if (DUAL && q * 64 >= 8 * cpr)  // rows 8..15: Wu (uniform: 8 cpr is a multiple of 64)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_w + q * 1024),
+                             "v"(off), "s"(rw2));
+            else
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_w + q * 1024),
+                             "v"(off), "s"(rw));
+        }
+    }
+    // X step st into stage slot: load j covers rows 8 j .. 8 j + 7, lane l
+    // row 8 j + l / 8 at position l % 8. Rows past M read as zero.
+    const i32x4 rx = make_rsrc(X, (uint32_t)((long)M * K * 2));
+    auto load_x = [&](int st, int slot) {
+        const int xr = lane >> 3, pos = lane & 7;
+#pragma unroll
+        for (int j = 0; j < XL; j++) {
+            const int r = 8 * j + xr;
+            const int c = pos ^ ((r >> 1) & 7);
+            const uint32_t off = (uint32_t)((r * K + k0 + 64 * st + 8 * c) * 2);
+            // (the clobber keeps the stage's earlier operand reads before it)
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_x + slot * XS + j * 1024),
+                         "v"(off), "s"(rx)
+                         : "memory");
+        }
+    };
+    const int mysteps = nst > wave ? (nst - wave + SK_WAVES - 1) / SK_WAVES : 0;
+#pragma unroll
+    for (int u = 0; u < XD; u++)
+        if (u < mysteps) load_x(wave + SK_WAVES * u, u);
+
+    float4v acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = float4v{};
+    const char* ldsc = reinterpret_cast<const char*>(lds);
+    const char* wrow = ldsc + row * KS * 2;
+    const char* xbase = ldsc + WB + wave * XD * XS;
+#pragma unroll
+    for (int u = 0; u < MAXU; u++) {
+        if (u >= mysteps) break;
+        // Wait for step u's X (later stages may still fly); the first wait
+        // also covers this wavefront's W loads, and the barrier everyone's.
+        const int ahead = min(XD - 1, mysteps - 1 - u);
+        if (ahead > 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(XL));
+        else __builtin_amdgcn_s_waitcnt(0x0f70);
+        asm volatile("" ::: "memory");  // no LDS read moves above the wait
+        if (u == 0) __syncthreads();
+        const int st = wave + SK_WAVES * u, slot = u % XD;
+        const char* xs = xbase + slot * XS;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = 8 * st + 4 * i + g;
+            const half8 w = *reinterpret_cast<const half8*>(wrow + 16 * (c ^ row));
+            const int xc = 4 * i + g;
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int r = 16 * t + row;
+                const half8 x = *reinterpret_cast<const half8*>(xs + r * 128 + 16 * (xc ^ ((r >> 1) & 7)));
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, x, acc[t], 0, 0, 0);
+            }
+        }
+        if (u + XD < mysteps) load_x(st + SK_WAVES * XD, slot);
+    }
+    if (mysteps == 0) __syncthreads();  // matches the barrier of wavefronts with steps
+    // Sum the 8 partial tiles through LDS in wavefront order; thread tid < 256
+    // keeps element tid (register tid/64 of lane tid%64) of each.
+    float sum[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[wave][r][lane] = acc[t][r];
+        __syncthreads();
+        float v = 0.0f;
+        if (tid < 256)
+#pragma unroll
+            for (int w = 0; w < SK_WAVES; w++) v += red[w][tid >> 6][tid & 63];
+        sum[t] = v;
+    }
+    // Element (r, l): block row 4 (l / 16) + r, m = 16 t + l % 16. For
+    // gate_up, rows 0..7 are gate rows and 8..15 their up partners, which
+    // sit 32 lanes on: exchanged through red.
+    const int r = tid >> 6, l = tid & 63;
+    float up[MT];
+    if constexpr (DUAL) {
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            __syncthreads();
+            if (tid < 256) red[0][r][l] = sum[t];
+            __syncthreads();
+            up[t] = tid < 256 && l < 32 ? red[0][r][l + 32] : 0.0f;
+        }
+        if (l >= 32) return;
+    }
+    if (tid >= 256) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const int n = n0 + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
+        if (m >= M || n >= N) continue;
+        const float v = sum[t], uu = DUAL ? up[t] : 0.0f;
+        if constexpr (SPLIT) {
+            float* pp = part + (size_t)ks * (DUAL ? 2 : 1) * M * N + (size_t)m * N + n;
+            pp[0] = v;
+            if constexpr (DUAL) pp[(size_t)M * N] = uu;
+        } else {
+            sk_store<EPI>(C, bias, N, m, n, v, uu);
+        }
+    }
+}
+
 // Sums the S slices of a split skinny product in slice order, then the epilogue.
 template <int EPI>
 __global__ __launch_bounds__(256) void skinny_reduce(const float* __restrict__ part, int S, int M, int N, void* C,
@@ -710,12 +873,18 @@ __global__ __launch_bounds__(256) void skinny_reduce(const float* __restrict__ p
 // The skinny path's shape plan: 16-row tiles per workgroup and K slices.
 struct SkPlan {
     bool use = false;
+    bool lds = false;  // gemm_skinny_lds (K % 128 == 0): slices of at most SL_KS
     int rt = 1, split = 1;
 };
 SkPlan sk_plan(bool bt, int M, int N, int K) {
     SkPlan p;
     if (!bt || M <= 0 || M > 64 || N <= 0 || K <= 0 || K % 64) return p;
     p.use = true;
+    if (K % 128 == 0) {
+        p.lds = true;
+        p.split = (K / 128 + SL_KS / 128 - 1) / (SL_KS / 128);
+        return p;
+    }
     p.rt = N >= 4096 ? 2 : 1;
     const int blocks = (N + 16 * p.rt - 1) / (16 * p.rt), nst = K / 64;
     // K slices only pay for their extra reduce launch when K is long and the
@@ -757,6 +926,21 @@ void launch_skinny_rt(const u16* X, const u16* W, const u16* W2, void* C, const 
 template <int EPI, int MT>
 void launch_skinny(const u16* X, const u16* W, const u16* W2, void* C, const u16* bias, int M, int N, int K,
                    const SkPlan& p, float* part, hipStream_t s, bool reduce = true) {
+    if (p.lds) {
+        const unsigned blocks = EPI == EPI_SWIGLU ? (N + 7) / 8 : (N + 15) / 16;
+        if (p.split > 1) {
+            hipLaunchKernelGGL((gemm_skinny_lds<EPI, MT, true>), dim3(blocks, p.split), dim3(64 * SK_WAVES), 0, s, X, W,
+                               W2, C, bias, M, N, K, part);
+            if (!reduce) return;
+            const long mn = (long)M * N;
+            hipLaunchKernelGGL(skinny_reduce<EPI>, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, p.split,
+                               M, N, C, bias);
+        } else {
+            hipLaunchKernelGGL((gemm_skinny_lds<EPI, MT, false>), dim3(blocks), dim3(64 * SK_WAVES), 0, s, X, W, W2, C,
+                               bias, M, N, K, part);
+        }
+        return;
+    }
     if (p.rt == 2) launch_skinny_rt<EPI, MT, 2>(X, W, W2, C, bias, M, N, K, p.split, part, s, reduce);
     else launch_skinny_rt<EPI, MT, 1>(X, W, W2, C, bias, M, N, K, p.split, part, s, reduce);
 }
