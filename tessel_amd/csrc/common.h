@@ -31,6 +31,14 @@ TSL_DEV float as_float(uint32_t x) { return __builtin_bit_cast(float, x); }
 TSL_DEV float h2f(u16 h) { return (float)__builtin_bit_cast(half_t, h); }
 TSL_DEV u16 f2h(float f) { return __builtin_bit_cast(u16, (half_t)f); }
 
+// The rotary pair (x1 c - x2 s, x2 c + x1 s) rounded to f16, with its
+// multiply-adds spelled out, so every kernel that rotates (rope_q, kv_write,
+// the fused QKV epilogue) produces the same bits.
+TSL_DEV void rope_rotate(float x1, float x2, float c, float s, u16& y1, u16& y2) {
+    y1 = f2h(__builtin_fmaf(x1, c, -(x2 * s)));
+    y2 = f2h(__builtin_fmaf(x2, c, x1 * s));
+}
+
 // Largest / sum over the 64 lanes of a wavefront, every lane receiving it.
 TSL_DEV float wave_max(float x) {
 #pragma unroll

@@ -294,17 +294,17 @@ struct Engine {
         std::memcpy(&eps_bits, &cfg.eps, 4);
         auto B = [](const Buf& b) { return Arg{Arg::BUF, b.p}; };
         Arg SC{Arg::F32, scale_bits}, EPS{Arg::F32, eps_bits};
-        int embed_k, norm_k, qkv_k, rope_k, att_k, gu_k, down_k;
+        int embed_k, norm_k, qkv_k, att_k, gu_k, down_k;
         TRY(kernel("embed", {{T}, {vv, dm}, {T, dm}}, {{"BD", std::min<int64_t>(bc, 1024)}}, 4, &embed_k));
         TRY(kernel("rmsnorm", {{T, dm}, {dm}, {T, dm}}, {{"BC", bc}}, 4, &norm_k));
         const Layer& l0 = layers[0];
-        TRY(mm("linear", {{T, dm}, {w, dm}, {T, w}}, false, {B(h), B(l0.wqkv), B(qkv)}, &qkv_k));
         int64_t npos = cfg.max_pos;
-        // llm/rope_q then llm/kv_write (src/llm/engine.rs launch order), as one launch.
-        TRY(kernel("rope_kv",
-                   {{T, w}, {T}, {T}, {npos, hd / 2}, {npos, hd / 2}, {T, nh, hd}, {ns, ng, hd}, {ns, ng, hd},
-                    {T, ng, hd}, {T, ng, hd}},
-                   {}, 1, &rope_k, "fused"));
+        // llm/linear (QKV), then llm/rope_q and llm/kv_write (src/llm/engine.rs
+        // launch order), as one launch sequence: fused/qkv_rope_kv.
+        TRY(kernel("qkv_rope_kv",
+                   {{T, dm}, {w, dm}, {T, w}, {T}, {T}, {npos, hd / 2}, {npos, hd / 2}, {T, nh, hd}, {ns, ng, hd},
+                    {ns, ng, hd}, {T, ng, hd}, {T, ng, hd}},
+                   {}, 4, &qkv_k, "fused"));
         if (prefill) {
             TRY(kernel("prefill_attention", {{T, nh, hd}, {T, ng, hd}, {T, ng, hd}, {T}, {T, nh, hd}},
                        {{"BM", 64}, {"BN", 64}}, 4, &att_k));
@@ -330,8 +330,8 @@ struct Engine {
         TRY(launch(norm_k, {B(x), B(layers[0].n1), B(h), EPS}));
         for (size_t li = 0; li < layers.size(); li++) {
             const Layer& L = layers[li];
-            TRY(launch(qkv_k, {B(h), B(L.wqkv), B(qkv)}));
-            TRY(launch(rope_k, {B(qkv), B(pos), B(slot), B(cos), B(sin), B(q), B(L.kc), B(L.vc), B(k), B(v)}));
+            TRY(launch(qkv_k, {B(h), B(L.wqkv), B(qkv), B(pos), B(slot), B(cos), B(sin), B(q), B(L.kc), B(L.vc), B(k),
+                               B(v)}));
             if (prefill) TRY(launch(att_k, {B(q), B(k), B(v), B(starts), B(o), SC}));
             else TRY(launch(att_k, {B(q), B(L.kc), B(L.vc), B(table), B(lens), B(o), SC}));
             TRY(launch(oproj_norm_k, {B(o), B(L.wo), B(x), B(L.n2), B(h), EPS}));

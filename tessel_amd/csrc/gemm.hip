@@ -44,7 +44,17 @@ TSL_DEV int swz(int row, int c) {
     return c ^ ((row ^ (row >> LG)) & (KC - 1));
 }
 
-enum Epi { EPI_F16 = 0, EPI_F32 = 1, EPI_RESID = 2, EPI_BIAS = 3, EPI_SWIGLU = 4 };
+enum Epi { EPI_F16 = 0, EPI_F32 = 1, EPI_RESID = 2, EPI_BIAS = 3, EPI_SWIGLU = 4, EPI_ROPE = 5 };
+
+// The fused QKV projection's epilogue (EPI_ROPE): llm.tl rope_q and kv_write
+// applied to the projection's f16-rounded outputs (column layout of QKV:
+// H query heads, G key heads, G value heads of D columns each).
+struct RopeEpi {
+    const int *pos = nullptr, *slot = nullptr;
+    const float *Cs = nullptr, *Sn = nullptr;
+    u16 *Q = nullptr, *Kc = nullptr, *Vc = nullptr, *K = nullptr, *V = nullptr;
+    int H = 0, G = 0, D = 0, D2 = 0, NS = 0, NPOS = 0;
+};
 
 // C tile mapping: workgroups are dispatched round-robin over the 8 XCDs, so
 // the id is first regrouped to give each XCD a contiguous run of tiles, and
@@ -708,15 +718,63 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const u16* __restri
 // Y^T (16 n x 16 m) += W (16 n x 32 k) X^T (32 k x 16 m) on
 // v_mfma_f32_16x16x32_f16; the 8 partial tiles are summed in LDS in
 // wavefront order, then the epilogue (or the split layout of gemm_skinny).
+// EPI_ROPE pairs rows the same way inside W: block b holds rotary pairs
+// 8 b .. 8 b + 7 (pair p: column h D + i and its partner h D + D2 + i, with
+// h = p / D2, i = p % D2), so N counts pairs and the epilogue rotates them.
 constexpr int SL_KS = 2048;
+
+// Rotary pair n of token m from its two projection sums: QKV's f16 rounding,
+// then llm.tl rope_q (query heads) or kv_write (key heads rotated, value
+// heads copied; both also into the paged cache at slot[m] when it is in
+// [0, NS)), with the arithmetic of rope_q_elem / kv_write_elem.
+TSL_DEV void rope_store(const RopeEpi& ep, int m, int n, float v1, float v2) {
+    const int h = n / ep.D2, i = n % ep.D2;
+    const u16 b1 = f2h(v1), b2 = f2h(v2);
+    const float x1 = h2f(b1), x2 = h2f(b2);
+    const int p = ep.pos[m];
+    const bool pin = p >= 0 && p < ep.NPOS;
+    if (h < ep.H + ep.G) {
+        const float c = pin ? ep.Cs[(size_t)p * ep.D2 + i] : 0.0f, s = pin ? ep.Sn[(size_t)p * ep.D2 + i] : 0.0f;
+        u16 y1, y2;
+        rope_rotate(x1, x2, c, s, y1, y2);
+        if (h < ep.H) {
+            u16* q = ep.Q + ((size_t)m * ep.H + h) * ep.D;
+            q[i] = y1;
+            q[ep.D2 + i] = y2;
+            return;
+        }
+        const int g = h - ep.H, at = ep.slot[m];
+        u16* kk = ep.K + ((size_t)m * ep.G + g) * ep.D;
+        kk[i] = y1;
+        kk[ep.D2 + i] = y2;
+        if (at >= 0 && at < ep.NS) {
+            u16* kc = ep.Kc + ((size_t)at * ep.G + g) * ep.D;
+            kc[i] = y1;
+            kc[ep.D2 + i] = y2;
+        }
+        return;
+    }
+    const int g = h - ep.H - ep.G, at = ep.slot[m];
+    u16* vv = ep.V + ((size_t)m * ep.G + g) * ep.D;
+    vv[i] = b1;
+    vv[ep.D2 + i] = b2;
+    if (at >= 0 && at < ep.NS) {
+        u16* vc = ep.Vc + ((size_t)at * ep.G + g) * ep.D;
+        vc[i] = b1;
+        vc[ep.D2 + i] = b2;
+    }
+}
+
 template <int MT>
 constexpr int sl_xdepth() { return MT <= 2 ? 2 : 1; }
 template <int EPI, int MT, bool SPLIT>
 __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __restrict__ X, const u16* __restrict__ W,
                                                                    const u16* __restrict__ W2, void* C,
                                                                    const u16* __restrict__ bias, int M, int N, int K,
-                                                                   float* __restrict__ part) {
-    constexpr bool DUAL = EPI == EPI_SWIGLU;
+                                                                   float* __restrict__ part, RopeEpi ep) {
+    constexpr bool ROPE = EPI == EPI_ROPE;
+    constexpr bool DUAL = EPI == EPI_SWIGLU || ROPE;  // paired rows: 8 + 8 per block
+    static_assert(!(ROPE && SPLIT), "the rotary epilogue needs whole sums");
     constexpr int WB = 16 * SL_KS * 2;           // LDS bytes of the W block
     constexpr int XS = 16 * MT * 128;            // LDS bytes of one X step
     constexpr int XD = sl_xdepth<MT>();          // X stages per wavefront
@@ -740,8 +798,10 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     {
         const int rows = min(DUAL ? 8 : 16, N - n0);
         const uint32_t range = (uint32_t)(((long)(rows - 1) * K + KS) * 2);
-        const i32x4 rw = make_rsrc(W + (size_t)n0 * K + k0, range);
-        const i32x4 rw2 = make_rsrc((DUAL ? W2 : W) + (size_t)n0 * K + k0, range);
+        // First rows of the block's two halves (rotary pairs: within one head of W).
+        const long ra = ROPE ? (long)(n0 / ep.D2) * ep.D + n0 % ep.D2 : n0;
+        const i32x4 rw = make_rsrc(W + ra * K + k0, range);
+        const i32x4 rw2 = make_rsrc(ROPE ? W + (ra + ep.D2) * K + k0 : (DUAL ? W2 : W) + (size_t)n0 * K + k0, range);
         const int nq = cpr / 4;
         for (int q = wave; q < nq; q += SK_WAVES) {
             const int p = 64 * q + lane, r = p / cpr, pos = p - r * cpr;
@@ -845,6 +905,10 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         const int n = n0 + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
         if (m >= M || n >= N) continue;
         const float v = sum[t], uu = DUAL ? up[t] : 0.0f;
+        if constexpr (ROPE) {
+            rope_store(ep, m, n, v, uu);
+            continue;
+        }
         if constexpr (SPLIT) {
             float* pp = part + (size_t)ks * (DUAL ? 2 : 1) * M * N + (size_t)m * N + n;
             pp[0] = v;
@@ -930,14 +994,14 @@ void launch_skinny(const u16* X, const u16* W, const u16* W2, void* C, const u16
         const unsigned blocks = EPI == EPI_SWIGLU ? (N + 7) / 8 : (N + 15) / 16;
         if (p.split > 1) {
             hipLaunchKernelGGL((gemm_skinny_lds<EPI, MT, true>), dim3(blocks, p.split), dim3(64 * SK_WAVES), 0, s, X, W,
-                               W2, C, bias, M, N, K, part);
+                               W2, C, bias, M, N, K, part, RopeEpi{});
             if (!reduce) return;
             const long mn = (long)M * N;
             hipLaunchKernelGGL(skinny_reduce<EPI>, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, p.split,
                                M, N, C, bias);
         } else {
             hipLaunchKernelGGL((gemm_skinny_lds<EPI, MT, false>), dim3(blocks), dim3(64 * SK_WAVES), 0, s, X, W, W2, C,
-                               bias, M, N, K, part);
+                               bias, M, N, K, part, RopeEpi{});
         }
         return;
     }
@@ -1108,12 +1172,53 @@ int launch_linear_residual_rmsnorm(TslKernel& k, const uint64_t* a, hipStream_t 
     return run_rmsnorm_f32(R, P<u16>(a[3]), P<u16>(a[4]), M, N, ncols, eps, s);
 }
 
+// fused/qkv_rope_kv (the engine's fusion, not a .tl kernel): llm/linear
+// QKV = X Wqkv^T, then llm/rope_q and llm/kv_write of that QKV, arguments X
+// [T, Dm], Wqkv [W, Dm], QKV [T, W], pos, slot, C, S, Q, Kc, Vc, K, V (the
+// kernels' own). Decode-sized batches (T <= 64, Dm % 128 == 0, Dm <= 2048,
+// D = 2 D2, D2 % 8 == 0, W = (H + 2 G) D) run one skinny product whose
+// epilogue rotates and stores (QKV is then left unwritten); the outputs are
+// the bits the three launches give. Other shapes launch the three.
+int launch_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s);
+int launch_qkv_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    const int T = k.dim("T"), W = k.dim("W"), Dm = k.dim("Dm");
+    RopeEpi ep;
+    ep.H = k.dim("H"), ep.G = k.dim("G"), ep.D = k.dim("D"), ep.D2 = k.dim("D2"), ep.NS = k.dim("NS");
+    ep.NPOS = k.dim("NPOS");
+    const SkPlan p = sk_plan(true, T, W, Dm);
+    const bool fused = p.use && p.lds && p.split == 1 && ep.D == 2 * ep.D2 && ep.D2 % 8 == 0 &&
+                       W == (ep.H + 2 * ep.G) * ep.D;
+    if (!fused) {
+        if (int e = gemm_dispatch<true, EPI_F16>(P<u16>(a[0]), P<u16>(a[1]), nullptr, P<void>(a[2]), nullptr, T, W, Dm,
+                                                 s, "qkv_rope_kv", reinterpret_cast<float*>(k.scratch)))
+            return e;
+        return launch_rope_kv(k, a + 2, s);
+    }
+    ep.pos = P<int>(a[3]), ep.slot = P<int>(a[4]), ep.Cs = P<float>(a[5]), ep.Sn = P<float>(a[6]);
+    ep.Q = P<u16>(a[7]), ep.Kc = P<u16>(a[8]), ep.Vc = P<u16>(a[9]), ep.K = P<u16>(a[10]), ep.V = P<u16>(a[11]);
+    const int pairs = W / 2;
+    const unsigned blocks = (pairs + 7) / 8;
+    const u16 *X = P<u16>(a[0]), *Wq = P<u16>(a[1]);
+    auto go = [&](auto mt) {
+        hipLaunchKernelGGL((gemm_skinny_lds<EPI_ROPE, decltype(mt)::value, false>), dim3(blocks), dim3(64 * SK_WAVES), 0,
+                           s, X, Wq, nullptr, nullptr, nullptr, T, pairs, Dm, nullptr, ep);
+    };
+    switch ((T + 15) / 16) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 3: go(std::integral_constant<int, 3>{}); break;
+        default: go(std::integral_constant<int, 4>{}); break;
+    }
+    return TSL_LAUNCHED("qkv_rope_kv");
+}
+
 // Sizes the split-K partials (the skinny path at decode-sized M, the 128 x 128
 // path at prefill-sized M) once, when the kernel is specialised: split x (2
 // for gate_up) x M x N floats.
 int prepare_projection(TslKernel& k) {
-    const bool dual = k.name == "gate_up";
-    const int64_t M = k.dim("M"), N = dual ? k.dim("F") : k.dim("N"), K = k.dim("K");
+    const bool dual = k.name == "gate_up", qkv = k.name == "qkv_rope_kv";
+    const int64_t M = qkv ? k.dim("T") : k.dim("M"), K = qkv ? k.dim("Dm") : k.dim("K");
+    const int64_t N = dual ? k.dim("F") : qkv ? k.dim("W") : k.dim("N");
     if (M > (1 << 20) || N > (1 << 30)) return 0;
     SkPlan p = sk_plan(true, (int)M, (int)N, (int)K);
     if (k.name == "linear_residual_rmsnorm") {

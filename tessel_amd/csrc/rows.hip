@@ -391,8 +391,10 @@ TSL_DEV void rope_q_elem(const RopeArgs& a, long e) {
     const float x1 = c1 < a.W ? h2f(a.QKV[(size_t)t * a.W + c1]) : 0.0f;
     const float x2 = c2 < a.W ? h2f(a.QKV[(size_t)t * a.W + c2]) : 0.0f;
     u16* q = a.Q + ((size_t)t * a.H + h) * a.D;
-    if (i < a.D) q[i] = f2h(x1 * c - x2 * s);
-    if (a.D2 + i < a.D) q[a.D2 + i] = f2h(x2 * c + x1 * s);
+    u16 y1, y2;
+    rope_rotate(x1, x2, c, s, y1, y2);
+    if (i < a.D) q[i] = y1;
+    if (a.D2 + i < a.D) q[a.D2 + i] = y2;
 }
 
 // kv_write: the rotated keys and the values of kv head g into the paged
@@ -413,7 +415,8 @@ TSL_DEV void kv_write_elem(const RopeArgs& a, long e) {
         const long c1 = k0 + i, c2 = k0 + a.D2 + i;
         const float x1 = (c1 >= 0 && c1 < a.W) ? h2f(a.QKV[(size_t)t * a.W + c1]) : 0.0f;
         const float x2 = (c2 >= 0 && c2 < a.W) ? h2f(a.QKV[(size_t)t * a.W + c2]) : 0.0f;
-        const u16 y1 = f2h(x1 * c - x2 * s), y2 = f2h(x2 * c + x1 * s);
+        u16 y1, y2;
+        rope_rotate(x1, x2, c, s, y1, y2);
         if (i < a.D) {
             if (ain) kc[i] = y1;
             kk[i] = y1;

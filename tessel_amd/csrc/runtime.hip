@@ -42,6 +42,7 @@ int launch_rope_q(TslKernel&, const uint64_t*, hipStream_t);
 int launch_kv_write(TslKernel&, const uint64_t*, hipStream_t);
 int launch_rope_kv(TslKernel&, const uint64_t*, hipStream_t);
 int launch_linear_residual_rmsnorm(TslKernel&, const uint64_t*, hipStream_t);
+int launch_qkv_rope_kv(TslKernel&, const uint64_t*, hipStream_t);
 int launch_flash_attention(TslKernel&, const uint64_t*, hipStream_t);
 int launch_prefill_attention(TslKernel&, const uint64_t*, hipStream_t);
 int launch_decode_attention(TslKernel&, const uint64_t*, hipStream_t);
@@ -121,6 +122,12 @@ std::vector<KernelDef> g_defs = {
     {"fused", "linear_residual_rmsnorm",
      "X: f16[M, K], W: f16[N, K], R: f32[M, N], Wn: f16[N], Y: f16[M, N], eps: f32", "BC = 2048", "",
      launch_linear_residual_rmsnorm, prepare_projection},
+    // Not a .tl kernel: llm/linear (QKV = X Wqkv^T), then llm/rope_q and
+    // llm/kv_write of that QKV (the engine's fusion; their arguments after X, Wqkv).
+    {"fused", "qkv_rope_kv",
+     "X: f16[T, Dm], Wqkv: f16[W, Dm], QKV: f16[T, W], pos: i32[T], slot: i32[T], C: f32[NPOS, D2], "
+     "S: f32[NPOS, D2], Q: f16[T, H, D], Kc: f16[NS, G, D], Vc: f16[NS, G, D], K: f16[T, G, D], V: f16[T, G, D]",
+     "", "D2 D", launch_qkv_rope_kv, prepare_projection},
     {"llm", "prefill_attention",
      "Q: f16[S, H, D], K: f16[S, G, D], V: f16[S, G, D], starts: i32[S], O: f16[S, H, D], scale: f32",
      "BM = 64, BN = 64", "D", launch_prefill_attention, prepare_attention},

@@ -416,6 +416,41 @@ def test_fused_linear_residual_rmsnorm(m, k, n, mode):
         np.testing.assert_array_equal(out[4].view(np.uint16), py.view(np.uint16))
 
 
+@pytest.mark.parametrize("cfgname,t", [("tinyllama", 1), ("tinyllama", 32), ("tinyllama", 40), ("tinyllama", 64),
+                                       ("tinyllama", 80), ("tiny", 16)])
+def test_fused_qkv_rope_kv(cfgname, t):
+    # The engine's fused launch (fused/qkv_rope_kv): llm/linear, then
+    # llm/rope_q and llm/kv_write of its QKV. Decode-sized TinyLlama batches
+    # run the one-kernel form (rotation in the projection's epilogue); t = 80
+    # and the tiny config (dim 64) launch the three. Either way Q, K, V and
+    # the cache are the bits of the three launches. Slots outside the cache
+    # and positions outside the tables are included.
+    _say("fused qkv_rope_kv", cfgname, t)
+    cfg = getattr(oracle.Config, cfgname)()
+    c, s = oracle.rope_tables(cfg)
+    H, G, D, dm, W = cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.dim, cfg.qkv()
+    r = oracle.Rng(21 + t)
+    x = r.tensor("f16", [t, dm], 1.0)
+    wq = r.tensor("f16", [W, dm], 1.0 / np.sqrt(dm))
+    pos = np.array([(i * 97) % cfg.max_pos for i in range(t)], np.int32)
+    pos[0] = cfg.max_pos + 5  # outside the tables: rotated values are 0
+    NS = 3 * t + 7
+    slot = np.array([(i * 7) % NS for i in range(t)], np.int32)
+    slot[-1] = NS  # dropped
+    if t > 1:
+        slot[-2] = -1
+    Kc = r.tensor("f16", [NS, G, D])
+    Vc = r.tensor("f16", [NS, G, D])
+    z = lambda *sh: np.zeros(sh, np.float16)
+    args = [x, wq, z(t, W), pos, slot, c, s, z(t, H, D), Kc, Vc, z(t, G, D), z(t, G, D)]
+    got = T.run("fused", "qkv_rope_kv", [a.copy() for a in args])
+    qkv = T.run("llm", "linear", [x, wq, z(t, W)], outputs=[2])[2]
+    want = T.run("fused", "rope_kv", [qkv, pos, slot, c, s, z(t, H, D), Kc.copy(), Vc.copy(), z(t, G, D), z(t, G, D)])
+    for gi, wi, name in ((7, 5, "Q"), (8, 6, "Kc"), (9, 7, "Vc"), (10, 8, "K"), (11, 9, "V")):
+        np.testing.assert_array_equal(got[gi].view(np.uint16), want[wi].view(np.uint16), err_msg=name)
+    parity("fused Q", got[7], oracle.rope_q(oracle.llm_linear(x, wq), pos, c, s, H, D))
+
+
 @pytest.mark.parametrize("cfgname", ["tiny", "tinyllama"])
 def test_rope_and_kv_write(cfgname):
     _say("rope/kv_write", cfgname)
