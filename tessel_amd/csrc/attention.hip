@@ -277,18 +277,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     }
 }
 
-int num_cus() {
-    static int n = 0;
-    if (!n) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-            n = v;
-        else
-            n = 256;
-    }
-    return n;
-}
 
 template <bool PREFILL>
 int run_attn(AttnArgs a, int D, hipStream_t s, const char* what) {

@@ -83,6 +83,9 @@ struct TslKernel {
 typedef int (*tsl_launcher)(TslKernel& k, const uint64_t* args, hipStream_t s);
 typedef int (*tsl_preparer)(TslKernel& k);  // optional: scratch sizing at tsl_kernel time
 
+// Compute units of the current device (runtime.hip; cached).
+int num_cus();
+
 // Records an argument/launch error (the C ABI's last error).
 int tsl_fail(int code, const std::string& msg);
 int tsl_hip_check(hipError_t e, const char* what);

@@ -919,6 +919,141 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     }
 }
 
+// The skinny product for many row blocks (more than the CUs: gate_up,
+// logits), persistent: one workgroup per CU walks blocks b, b + gridDim.x,
+// ... Wavefront w always owns the same contiguous K steps (K / 512 of them,
+// K = 1024 or 2048), so its X operands are loaded once into registers; per
+// block it streams its 512-byte segment of each of the 16 W rows (whole
+// lines, 2 rows per 1 KB direct-to-LDS load) into its own 2-slot LDS ring,
+// the next block's loads in flight while it computes. Block layout, MFMA,
+// reduction and epilogue are gemm_skinny_lds's (M <= 32).
+template <int EPI, int MT>
+__global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __restrict__ X, const u16* __restrict__ W,
+                                                                   const u16* __restrict__ W2, void* C,
+                                                                   const u16* __restrict__ bias, int M, int N, int K) {
+    constexpr bool DUAL = EPI == EPI_SWIGLU;
+    constexpr int SPW = 4;                   // most k steps per wavefront (K <= 2048)
+    constexpr int SLOT = 16 * SPW * 128;     // LDS bytes of one block's segments
+    static_assert(MT <= 2, "X stays in registers");
+    __shared__ __attribute__((aligned(16))) u16 lds[SK_WAVES * 2 * SLOT / 2];
+    __shared__ float red[SK_WAVES][4][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row = lane & 15, g = lane >> 4;
+    const int nsw = K / 512;                 // k steps of this wavefront: nsw * wave ..
+    const int kw = 64 * nsw * wave;          // its first k
+    const int cpr = 8 * nsw;                 // 16-byte chunks per row segment (16 or 32)
+    const int nl = 2 * nsw;                  // 1 KB loads per block
+    const int rpb = DUAL ? 8 : 16;
+    const int nblk = (N + rpb - 1) / rpb;
+    const uint32_t ring = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds) + wave * 2 * SLOT;
+
+    // X operands of this wavefront's steps (rows past M are zero).
+    const u32x4 z = {0, 0, 0, 0};
+    u32x4 xv[SPW][MT][2];
+#pragma unroll
+    for (int j = 0; j < SPW; j++)
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const bool ok = j < nsw && 16 * t + row < M;
+            const u16* xp = X + (size_t)(ok ? 16 * t + row : 0) * K + kw + 64 * j + 8 * g;
+#pragma unroll
+            for (int i = 0; i < 2; i++) xv[j][t][i] = ok ? ldg16(xp + 32 * i) : z;
+        }
+    // W segments of block b into ring slot: load q covers chunks 64 q ..
+    // 64 q + 63 (row p / cpr, position p % cpr, holding chunk pos ^ (row & 15)).
+    auto load_w = [&](int b, int slot) {
+        const int n0 = b * rpb, rows = min(rpb, N - n0);
+        const uint32_t range = (uint32_t)(((long)(rows - 1) * K + K - kw) * 2);
+        const i32x4 rw = make_rsrc(W + (size_t)n0 * K + kw, range);
+        const i32x4 rw2 = make_rsrc((DUAL ? W2 : W) + (size_t)n0 * K + kw, range);
+        for (int q = 0; q < nl; q++) {
+            const int p = 64 * q + lane, r = p / cpr, pos = p - r * cpr;
+            const int rr = DUAL ? r & 7 : r;
+            const uint32_t off = (uint32_t)((rr * K + 8 * (pos ^ (r & 15))) * 2);
+            if (DUAL && q >= nl / 2)  // rows 8..15: Wu
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(ring + slot * SLOT + q * 1024),
+                             "v"(off), "s"(rw2)
+                             : "memory");
+            else
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(ring + slot * SLOT + q * 1024),
+                             "v"(off), "s"(rw)
+                             : "memory");
+        }
+    };
+    const int b0 = blockIdx.x, bs = gridDim.x;
+    if (b0 < nblk) load_w(b0, 0);
+    if (b0 + bs < nblk) load_w(b0 + bs, 1);
+    const char* ldsc = reinterpret_cast<const char*>(lds) + wave * 2 * SLOT;
+    int slot = 0;
+    for (int b = b0; b < nblk; b += bs, slot ^= 1) {
+        // Wait for this block's segments (the next block's may still fly).
+        if (b + bs < nblk) {
+            if (nl == 8) __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(4));
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0f70);
+        }
+        asm volatile("" ::: "memory");
+        float4v acc[MT];
+#pragma unroll
+        for (int t = 0; t < MT; t++) acc[t] = float4v{};
+        const char* wrow = ldsc + slot * SLOT + row * cpr * 16;
+#pragma unroll
+        for (int j = 0; j < SPW; j++) {
+            if (j >= nsw) break;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int c = 8 * j + 4 * i + g;
+                const half8 w = *reinterpret_cast<const half8*>(wrow + 16 * (c ^ row));
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, __builtin_bit_cast(half8, xv[j][t][i]), acc[t], 0,
+                                                                  0, 0);
+            }
+        }
+        // Sum the 8 partial tiles in wavefront order (thread tid < 256: element
+        // tid), then gate_up's partner exchange and the epilogue.
+        float sum[MT];
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[wave][r][lane] = acc[t][r];
+            __syncthreads();
+            float v = 0.0f;
+            if (tid < 256)
+#pragma unroll
+                for (int w = 0; w < SK_WAVES; w++) v += red[w][tid >> 6][tid & 63];
+            sum[t] = v;
+        }
+        const int r = tid >> 6, l = tid & 63;
+        float up[MT];
+        if constexpr (DUAL) {
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                __syncthreads();
+                if (tid < 256) red[0][r][l] = sum[t];
+                __syncthreads();
+                up[t] = tid < 256 && l < 32 ? red[0][r][l + 32] : 0.0f;
+            }
+        }
+        if (tid < 256 && (!DUAL || l < 32)) {
+            const int n0 = b * rpb;
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int n = n0 + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
+                if (m >= M || n >= N) continue;
+                sk_store<EPI>(C, bias, N, m, n, sum[t], DUAL ? up[t] : 0.0f);
+            }
+        }
+        // The block after next into the slot just read. Issued after the
+        // epilogue's stores (which also count in vmcnt), so the next wait
+        // leaves exactly these loads in flight.
+        if (b + 2 * bs < nblk) load_w(b + 2 * bs, slot);
+    }
+}
+
 // Sums the S slices of a split skinny product in slice order, then the epilogue.
 template <int EPI>
 __global__ __launch_bounds__(256) void skinny_reduce(const float* __restrict__ part, int S, int M, int N, void* C,
@@ -992,6 +1127,13 @@ void launch_skinny(const u16* X, const u16* W, const u16* W2, void* C, const u16
                    const SkPlan& p, float* part, hipStream_t s, bool reduce = true) {
     if (p.lds) {
         const unsigned blocks = EPI == EPI_SWIGLU ? (N + 7) / 8 : (N + 15) / 16;
+        if constexpr (MT <= 2) {
+            if (p.split == 1 && blocks > (unsigned)num_cus() && (K == 1024 || K == 2048)) {
+                hipLaunchKernelGGL((gemm_skinny_pst<EPI, MT>), dim3(num_cus()), dim3(64 * SK_WAVES), 0, s, X, W, W2, C,
+                                   bias, M, N, K);
+                return;
+            }
+        }
         if (p.split > 1) {
             hipLaunchKernelGGL((gemm_skinny_lds<EPI, MT, true>), dim3(blocks, p.split), dim3(64 * SK_WAVES), 0, s, X, W,
                                W2, C, bias, M, N, K, part, RopeEpi{});

@@ -51,6 +51,20 @@ int prepare_attention(TslKernel&);
 int prepare_decode(TslKernel&);
 int prepare_projection(TslKernel&);
 
+// Compute units of the current device (cached; 256 if the query fails).
+int num_cus() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
 namespace {
 
 thread_local std::string g_err;

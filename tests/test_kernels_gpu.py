@@ -128,11 +128,12 @@ def test_llm_matmuls_tinyllama_shapes(name, m):
 
 @pytest.mark.parametrize("name", MM_CASES)
 @pytest.mark.parametrize("m,k,n", [(40, 192, 100), (7, 4160, 33), (64, 64, 1), (40, 2176, 100), (3, 384, 17),
-                                   (17, 4352, 50)])
+                                   (17, 4352, 50), (32, 2048, 5000), (20, 1024, 4500)])
 def test_llm_matmuls_ragged_few_rows(name, m, k, n):
     # Few-row (decode-sized) products with ragged M and N, one K step, a long
     # K that is split across workgroups, and (K % 128 == 0) the LDS-staged
-    # blocks with uneven K slices and a partial last block of rows.
+    # blocks with uneven K slices and a partial last block of rows; more
+    # blocks than CUs at K = 1024 or 2048 take the persistent form.
     _say("llm mm ragged", name, m, k, n)
     r = oracle.Rng(300 + m + n)
     args, want = _mm_args(r, name, m, k, n, wscale=1.0 / np.sqrt(k))
