@@ -86,6 +86,10 @@ int tsl_launch(int handle, const uint64_t* args, int nargs);
 /* Event-timed milliseconds of `iters` launches of handle (after the stream
  * drains); ms receives the total. */
 int tsl_time_launches(int handle, const uint64_t* args, int nargs, int iters, float* ms);
+/* Each of `iters` launches of handle timed on its own with a pair of events
+ * (Cuda::time, src/driver.rs:365-380, as Compiled::time uses it,
+ * src/runtime.rs:294-316): ms[i] receives launch i's milliseconds. */
+int tsl_time_each(int handle, const uint64_t* args, int nargs, int iters, float* ms);
 /* Starts recording this thread's launches on the stream into a graph
  * (relaxed capture mode, src/driver.rs:340-348). */
 int tsl_capture_begin(void);
@@ -110,6 +114,14 @@ typedef struct {
 typedef struct {
     int32_t page, pages, max_tokens, max_seq_pages;
 } tsl_limits;
+
+/* bench::Rng (src/bench.rs:13-35), the xorshift generator of the benchmark
+ * suite's inputs: Rng::new(seed) into *state; bits() into *out; tensor(dtype,
+ * n, scale) into out as n f32 (dtype 0) or f16 bits rounded to nearest even
+ * (dtype 1). The state advances as the reference's does. */
+int tsl_rng_new(uint64_t seed, uint64_t* state);
+int tsl_rng_bits(uint64_t* state, uint64_t* out);
+int tsl_rng_tensor(uint64_t* state, size_t n, float scale, int dtype, void* out);
 
 /* Weights::random(cfg, seed) (src/llm/mod.rs:80-108) into host arrays of
  * f16 bits: embed[vocab*dim], per layer (attn_norm[dim],
@@ -140,13 +152,16 @@ int tsl_engine_step(int engine, int n, const int32_t* tokens, const int32_t* pos
  * tokens). out_tokens gets sum(max_new) slots: request r's tokens start at
  * the prefix sum of max_new; out_counts[r] is how many it produced.
  * stats: prefill_steps, decode_steps, prompt_tokens, generated,
- * largest_batch, decode_tokens (int64) and seconds, decode_seconds. */
+ * largest_batch, decode_tokens (int64) and seconds, decode_seconds.
+ * out_times (may be NULL): 2 nreq doubles, request r's Output::first_token_s
+ * and done_s (seconds from the start of the call, src/llm/sched.rs:14-20). */
 typedef struct {
     int64_t prefill_steps, decode_steps, prompt_tokens, generated, largest_batch, decode_tokens;
     double seconds, decode_seconds;
 } tsl_stats;
 int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* offsets, const int32_t* max_new,
-                 int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats);
+                 int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats,
+                 double* out_times);
 
 /* ---- checkpoints (src/llm/safetensors.rs) */
 

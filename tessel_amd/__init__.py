@@ -46,7 +46,8 @@ EXPORTS = [
     "tsl_time_launches", "tsl_capture_begin", "tsl_capture_end", "tsl_replay", "tsl_event_record",
     "tsl_event_elapsed", "tsl_weights_sizes", "tsl_weights_random", "tsl_engine_new", "tsl_engine_free",
     "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
-    "tsl_checkpoint_save", "tsl_json_roundtrip",
+    "tsl_checkpoint_save", "tsl_json_roundtrip", "tsl_rng_new", "tsl_rng_bits", "tsl_rng_tensor",
+    "tsl_time_each",
 ]
 
 
@@ -110,11 +111,15 @@ def _declare(L):
     L.tsl_engine_free.argtypes = [_INT]
     L.tsl_engine_set.argtypes = [_INT, _INT, _INT]
     L.tsl_engine_step.argtypes = [_INT, _INT, _P, _P, _P, _INT, _P, _INT, _P, _P, _INT, _P, _P]
-    L.tsl_generate.argtypes = [_INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, ctypes.POINTER(Stats)]
+    L.tsl_generate.argtypes = [_INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, ctypes.POINTER(Stats), _P]
     L.tsl_checkpoint_config.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config)]
     L.tsl_checkpoint_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config), _P, _P, _P, _P, ctypes.POINTER(_INT)]
     L.tsl_checkpoint_save.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config), _P, _P, _P, _P]
     L.tsl_json_roundtrip.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    L.tsl_time_each.argtypes = [_INT, ctypes.POINTER(_U64), _INT, _INT, _P]
+    L.tsl_rng_new.argtypes = [_U64, ctypes.POINTER(_U64)]
+    L.tsl_rng_bits.argtypes = [ctypes.POINTER(_U64), ctypes.POINTER(_U64)]
+    L.tsl_rng_tensor.argtypes = [ctypes.POINTER(_U64), ctypes.c_size_t, ctypes.c_float, _INT, _P]
 
 
 def check(rc):
@@ -218,6 +223,14 @@ def time_launches(k, args, iters):
     ms = ctypes.c_float()
     check(lib().tsl_time_launches(k.handle, _raw(args), len(args), int(iters), ctypes.byref(ms)))
     return ms.value
+
+
+def time_each(k, args, iters):
+    """Milliseconds of each of `iters` launches, each timed on its own."""
+    raw = _raw(args)
+    ms = np.zeros(max(iters, 1), np.float32)
+    check(lib().tsl_time_each(k.handle, raw, len(args), iters, ms.ctypes.data))
+    return ms[:iters].tolist()
 
 
 def sync():
@@ -431,7 +444,8 @@ class Engine:
 
     def generate(self, requests, max_batch, packed=True):
         """sched::generate_with: requests = [(prompt tokens, max_new)] ->
-        (token lists, Stats)."""
+        (token lists, Stats). Afterwards self.first_token_s and self.done_s
+        hold each request's Output times (src/llm/sched.rs:14-20)."""
         prompts = _i32([t for p, _ in requests for t in p])
         offsets = np.zeros(len(requests) + 1, np.int64)
         offsets[1:] = np.cumsum([len(p) for p, _ in requests])
@@ -439,14 +453,42 @@ class Engine:
         out = np.zeros(max(int(max_new.sum()), 1), np.int32)
         counts = np.zeros(len(requests), np.int32)
         st = Stats()
+        times = np.zeros(2 * max(len(requests), 1), np.float64)
         check(lib().tsl_generate(self.handle, len(requests), prompts.ctypes.data, offsets.ctypes.data,
                                  max_new.ctypes.data, int(max_batch), int(packed), out.ctypes.data,
-                                 counts.ctypes.data, ctypes.byref(st)))
+                                 counts.ctypes.data, ctypes.byref(st), times.ctypes.data))
+        self.first_token_s = times[0:2 * len(requests):2].tolist()
+        self.done_s = times[1:2 * len(requests):2].tolist()
         res, base = [], 0
         for i, m in enumerate(max_new):
             res.append(out[base:base + counts[i]].tolist())
             base += int(m)
         return res, st
+
+
+class Rng:
+    """bench::Rng (src/bench.rs:13-35), the xorshift generator of the
+    benchmark suite's inputs, through the library (tsl_rng_*)."""
+
+    def __init__(self, seed):
+        self.state = _U64(0)
+        check(lib().tsl_rng_new(seed, ctypes.byref(self.state)))
+
+    def bits(self):
+        out = _U64(0)
+        check(lib().tsl_rng_bits(ctypes.byref(self.state), ctypes.byref(out)))
+        return out.value
+
+    def below(self, n):
+        return self.bits() % n
+
+    def tensor(self, dtype, shape, scale=1.0):
+        """Rng::tensor: uniform [-1, 1) times scale, as 'f32' or 'f16'."""
+        n = int(np.prod(shape)) if len(shape) else 1
+        code, npdt = {"f32": (0, np.float32), "f16": (1, np.float16)}[dtype]
+        out = np.empty(n, npdt)
+        check(lib().tsl_rng_tensor(ctypes.byref(self.state), n, scale, code, out.ctypes.data))
+        return out.reshape(shape)
 
 
 def padded(n):

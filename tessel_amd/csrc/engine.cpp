@@ -439,6 +439,35 @@ int tsl_weights_sizes(const tsl_config* cfg, size_t* embed, size_t* per_layer, s
     return 0;
 }
 
+// bench::Rng (src/bench.rs:13-35): the generator behind the benchmark
+// suite's inputs, for the command line's bench.
+int tsl_rng_new(uint64_t seed, uint64_t* state) {
+    if (!state) return tsl_fail(TSL_ERR_ARG, "null state");
+    *state = Rng(seed).s;
+    return 0;
+}
+int tsl_rng_bits(uint64_t* state, uint64_t* out) {
+    if (!state || !out) return tsl_fail(TSL_ERR_ARG, "null state");
+    Rng r(0);
+    r.s = *state;
+    *out = r.bits();
+    *state = r.s;
+    return 0;
+}
+int tsl_rng_tensor(uint64_t* state, size_t n, float scale, int dtype, void* out) {
+    if (!state || (!out && n)) return tsl_fail(TSL_ERR_ARG, "null state or output");
+    if (dtype != 0 && dtype != 1) return tsl_fail(TSL_ERR_ARG, "dtype must be 0 (f32) or 1 (f16)");
+    Rng r(0);
+    r.s = *state;
+    for (size_t i = 0; i < n; i++) {
+        const float v = r.uniform() * scale;
+        if (dtype == 0) static_cast<float*>(out)[i] = v;
+        else static_cast<u16*>(out)[i] = to_f16(v);
+    }
+    *state = r.s;
+    return 0;
+}
+
 // Weights::random (src/llm/mod.rs:80-108).
 int tsl_weights_random(const tsl_config* cfg, uint64_t seed, uint16_t* embed, uint16_t* layers, uint16_t* norm,
                        uint16_t* head) {
@@ -519,7 +548,8 @@ int tsl_engine_step(int engine, int n, const int32_t* tokens, const int32_t* pos
 
 // sched::generate_with (src/llm/sched.rs:52-179).
 int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* offsets, const int32_t* max_new,
-                 int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats) {
+                 int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats,
+                 double* out_times) {
     Engine* e = get(engine);
     if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
     using clk = std::chrono::steady_clock;
@@ -545,7 +575,16 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
     tsl_stats st{};
     max_batch = std::min(max_batch, e->lim.max_tokens);
     const int eos = e->cfg.eos;
-    auto emit = [&](int id, int32_t t) { out_tokens[out_base[id] + out_counts[id]++] = t; };
+    auto since = [&]() { return std::chrono::duration<double>(clk::now() - start).count(); };
+    if (out_times)
+        for (int i = 0; i < 2 * nreq; i++) out_times[i] = 0.0;
+    auto emit = [&](int id, int32_t t) {
+        out_tokens[out_base[id] + out_counts[id]++] = t;
+        if (out_times && out_counts[id] == 1) out_times[2 * id] = since();  // first_token_s
+    };
+    auto done = [&](int id) {
+        if (out_times) out_times[2 * id + 1] = since();  // done_s
+    };
     while (!waiting.empty() || !running.empty()) {
         std::vector<std::pair<int, std::vector<int32_t>>> admit;
         size_t tokens = 0;
@@ -596,6 +635,7 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
                 size_t plen = (size_t)(offsets[id + 1] - offsets[id]);
                 Seq s{id, admit[i].second, plen, t, max_new[id] - 1};
                 if (s.left == 0 || t == eos) {
+                    done(id);
                     free_pages.insert(free_pages.end(), s.pages.begin(), s.pages.end());
                 } else {
                     running.push_back(s);
@@ -631,6 +671,7 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
             s.left--;
             emit(s.id, t);
             if (s.left == 0 || t == eos) {
+                done(s.id);
                 free_pages.insert(free_pages.end(), s.pages.begin(), s.pages.end());
             } else {
                 keep.push_back(s);

@@ -490,16 +490,35 @@ int tsl_time_launches(int handle, const uint64_t* args, int nargs, int iters, fl
     CHECK(hipEventCreate(&b), "event");
     CHECK(hipStreamSynchronize(g.stream), "sync");
     CHECK(hipEventRecord(a, g.stream), "record");
-    for (int i = 0; i < iters; i++) {
-        int r = tsl_launch(handle, args, nargs);
-        if (r) return r;
-    }
-    CHECK(hipEventRecord(b, g.stream), "record");
-    CHECK(hipEventSynchronize(b), "event sync");
-    CHECK(hipEventElapsedTime(ms, a, b), "elapsed");
+    int r = 0;
+    for (int i = 0; i < iters && !r; i++) r = tsl_launch(handle, args, nargs);
+    if (!r) r = tsl_hip_check(hipEventRecord(b, g.stream), "record");
+    if (!r) r = tsl_hip_check(hipEventSynchronize(b), "event sync");
+    if (!r) r = tsl_hip_check(hipEventElapsedTime(ms, a, b), "elapsed");
     (void)hipEventDestroy(a);
     (void)hipEventDestroy(b);
-    return 0;
+    return r;
+}
+
+// Cuda::time around one launch, `iters` times (src/driver.rs:365-380, as
+// Compiled::time uses it, src/runtime.rs:294-316): ms[i] is launch i's time.
+int tsl_time_each(int handle, const uint64_t* args, int nargs, int iters, float* ms) {
+    NEED_OPEN();
+    if (iters > 0 && !ms) return tsl_fail(TSL_ERR_ARG, "null ms");
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a), "event");
+    CHECK(hipEventCreate(&b), "event");
+    int r = 0;
+    for (int i = 0; i < iters && !r; i++) {
+        r = tsl_hip_check(hipEventRecord(a, g.stream), "record");
+        if (!r) r = tsl_launch(handle, args, nargs);
+        if (!r) r = tsl_hip_check(hipEventRecord(b, g.stream), "record");
+        if (!r) r = tsl_hip_check(hipEventSynchronize(b), "event sync");
+        if (!r) r = tsl_hip_check(hipEventElapsedTime(&ms[i], a, b), "elapsed");
+    }
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return r;
 }
 
 int tsl_capture_begin(void) {
