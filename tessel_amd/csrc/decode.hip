@@ -20,7 +20,7 @@
 namespace {
 
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr int DEC_MAX_CHUNK = 16;  // pages per chunk of a long table, at most
+constexpr int DEC_MAX_CHUNK = 24;  // pages per chunk of a long table, at most
 constexpr int DEC_WIDE_MAX_PAGES = 64;  // tables up to this many pages: one chunk per sequence
 
 struct DecArgs {
@@ -585,7 +585,7 @@ int run_decode_d(DecArgs& a, int qpg, hipStream_t s) {
 // Pages per chunk: enough chunks for about 2048 workgroups over B x G at the
 // table's full length (short contexts get short chunks, so the cache is
 // still read by the whole chip), few enough that one (b, g)'s chunk states
-// fit the merge's 64 KB of LDS; between 2 and 16 pages.
+// fit the merge's 64 KB of LDS; between 2 and 24 pages.
 int chunk_pages(const TslKernel& k) {
     const int64_t H = k.dim("H"), G = k.name == "paged_attention" ? H : k.dim("G");
     const int64_t bg = std::max<int64_t>(1, k.dim("B") * G), mp = k.dim("MP");
