@@ -1,7 +1,8 @@
 // The LLM engine on the C ABI: a Llama-family decoder whose GPU work is
 // only the llm.tl kernels, with a paged KV cache and continuous batching.
 //
-//   Config / Weights::random / rope_tables / argmax   src/llm/mod.rs:15-140
+//   Config / Weights::random / rope_tables            src/llm/mod.rs:15-129
+//   (argmax, :132-140, is the GPU's fused/argmax)
 //   Engine::new / mm (tuner) / step / launch_all      src/llm/engine.rs:150-529
 //   sched::generate_with                              src/llm/sched.rs:52-179
 //
@@ -61,13 +62,6 @@ void rope_tables(const tsl_config& c, std::vector<float>& cs, std::vector<float>
             cs[p * h + i] = (float)std::cos(a);
             sn[p * h + i] = (float)std::sin(a);
         }
-}
-
-size_t argmax(const float* xs, size_t n) {
-    size_t best = 0;
-    for (size_t i = 0; i < n; i++)
-        if (xs[i] > xs[best]) best = i;
-    return best;
 }
 
 // ---------------------------------------------------------------- the engine
@@ -130,7 +124,19 @@ struct Engine {
     std::map<std::string, int> tuned;
     Buf embed, head, norm, cos, sin;
     std::vector<Layer> layers;
-    Buf x, h, qkv, q, k, v, o, mlp, last, logits, tok, pos, slot, idx, table, lens, starts;
+    Buf x, h, qkv, q, k, v, o, mlp, last, logits, tok, pos, slot, idx, table, lens, starts, next;
+    // One device arena for a step's inputs, filled by one upload: for a step
+    // of t (padded) rows, tok, pos, slot, idx, starts, lens (t ints each),
+    // then table (t max_seq_pages ints). layout(t) points the buffers there;
+    // the addresses depend only on t, so a graph captured for t stays valid.
+    Buf in;
+    std::vector<int32_t> hin;
+    void layout(size_t t) {
+        const size_t mp = lim.max_seq_pages;
+        Buf* parts[] = {&tok, &pos, &slot, &idx, &starts, &lens};
+        for (int i = 0; i < 6; i++) *parts[i] = Buf{in.p + (uint64_t)i * t * 4, t * 4};
+        table = Buf{in.p + 6 * t * 4, t * mp * 4};
+    }
 
     int alloc(size_t bytes, Buf& b) {
         b.bytes = bytes;
@@ -271,13 +277,8 @@ struct Engine {
         TRY(alloc(t * ff * 2, mlp));
         TRY(alloc(t * d * 2, last));
         TRY(alloc(t * (size_t)cfg.vocab * 4, logits));
-        TRY(alloc(t * 4, tok));
-        TRY(alloc(t * 4, pos));
-        TRY(alloc(t * 4, slot));
-        TRY(alloc(t * 4, idx));
-        TRY(alloc(t * (size_t)lim.max_seq_pages * 4, table));
-        TRY(alloc(t * 4, lens));
-        TRY(alloc(t * 4, starts));
+        TRY(alloc(t * (6 + (size_t)lim.max_seq_pages) * 4, in));
+        TRY(alloc(t * 4, next));
         return 0;
     }
 
@@ -346,15 +347,20 @@ struct Engine {
         int64_t BW = (int64_t)bw;
         TRY(kernel("rmsnorm_rows", {{T, dm}, {BW}, {dm}, {BW, dm}}, {{"BC", bc}}, 4, &fin_k));
         TRY(mm("logits", {{BW, dm}, {vv, dm}, {BW, vv}}, false, {B(last), B(head), B(logits)}, &head_k));
+        // The scheduler's argmax on the GPU (fused/argmax), so a step can
+        // return token ids instead of logits.
+        int am_k;
+        TRY(kernel("argmax", {{BW, vv}, {BW}}, {}, 4, &am_k, "fused"));
         TRY(launch(fin_k, {B(x), B(idx), B(norm), B(last), EPS}));
         TRY(launch(head_k, {B(last), B(head), B(logits)}));
+        TRY(launch(am_k, {B(logits), B(next)}));
         return 0;
     }
 
     // Engine::step (src/llm/engine.rs:275-354).
     int step(size_t n, const int32_t* tokens, const int32_t* ps_in, const int32_t* slots, int mode,
              const int32_t* st_in, size_t nseq, const int32_t* tables, const int32_t* ln_in, size_t nwant,
-             const int32_t* want, float* out) {
+             const int32_t* want, float* out, int32_t* out_tok = nullptr) {
         if (n == 0 || n > (size_t)lim.max_tokens) {
             std::ostringstream e;
             e << "a step of " << n << " tokens (at most " << lim.max_tokens << ")";
@@ -362,40 +368,34 @@ struct Engine {
         }
         size_t t = padded(n);
         int32_t ns = lim.pages * lim.page;
-        std::vector<int32_t> tk(tokens, tokens + n), ps(ps_in, ps_in + n), sl(slots, slots + n);
-        tk.resize(t, 0);
-        ps.resize(t, 0);
-        sl.resize(t, ns);  // padding rows write to no slot
-        TRY(write(tok, 0, tk.data(), t * 4));
-        TRY(write(pos, 0, ps.data(), t * 4));
-        TRY(write(slot, 0, sl.data(), t * 4));
         size_t mp = lim.max_seq_pages;
-        if (mode == PREFILL || mode == PACKED) {
-            std::vector<int32_t> st(n, 0);
-            if (mode == PACKED) {
-                if (!st_in) return tsl_fail(TSL_ERR_ARG, "packed prefill: one start per token");
-                st.assign(st_in, st_in + n);
-            }
-            for (size_t i = n; i < t; i++) st.push_back((int32_t)i);  // padding rows start at themselves
-            TRY(write(starts, 0, st.data(), t * 4));
-        } else if (mode == DECODE) {
-            if (nseq > t) return tsl_fail(TSL_ERR_ARG, "decode: more sequences than rows");
-            std::vector<int32_t> tb(t * mp, 0), ln(t, 0);
-            for (size_t b = 0; b < nseq; b++) {
-                std::memcpy(&tb[b * mp], tables + b * mp, mp * 4);
-                ln[b] = ln_in[b];
-            }
-            TRY(write(table, 0, tb.data(), tb.size() * 4));
-            TRY(write(lens, 0, ln.data(), ln.size() * 4));
-        } else {
-            return tsl_fail(TSL_ERR_ARG, "unknown attention mode");
-        }
         size_t bw = nwant ? padded(nwant) : 0;
-        if (bw) {
-            std::vector<int32_t> ix(want, want + nwant);
-            ix.resize(bw, 0);
-            TRY(write(idx, 0, ix.data(), bw * 4));
+        if (mode != PREFILL && mode != PACKED && mode != DECODE) return tsl_fail(TSL_ERR_ARG, "unknown attention mode");
+        if (mode == PACKED && !st_in) return tsl_fail(TSL_ERR_ARG, "packed prefill: one start per token");
+        if (mode == DECODE && nseq > t) return tsl_fail(TSL_ERR_ARG, "decode: more sequences than rows");
+        if (bw > t) return tsl_fail(TSL_ERR_ARG, "more logits rows than step rows");
+        // Every input of the step in the arena's layout for t, one upload.
+        layout(t);
+        const size_t nin = 6 * t + (mode == DECODE ? t * mp : 0);
+        hin.assign(nin, 0);
+        int32_t *h_tok = &hin[0], *h_pos = &hin[t], *h_slot = &hin[2 * t], *h_idx = &hin[3 * t];
+        int32_t *h_st = &hin[4 * t], *h_len = &hin[5 * t];
+        std::copy(tokens, tokens + n, h_tok);
+        std::copy(ps_in, ps_in + n, h_pos);
+        std::copy(slots, slots + n, h_slot);
+        std::fill(h_slot + n, h_slot + t, ns);  // padding rows write to no slot
+        if (bw) std::copy(want, want + nwant, h_idx);
+        if (mode == PREFILL || mode == PACKED) {
+            if (mode == PACKED) std::copy(st_in, st_in + n, h_st);
+            for (size_t i = n; i < t; i++) h_st[i] = (int32_t)i;  // padding rows start at themselves
+        } else {
+            int32_t* h_tb = &hin[6 * t];
+            for (size_t b = 0; b < nseq; b++) {
+                std::memcpy(h_tb + b * mp, tables + b * mp, mp * 4);
+                h_len[b] = ln_in[b];
+            }
         }
+        TRY(write(in, 0, hin.data(), nin * 4));
         bool prefill = mode != DECODE;
         if (!prefill && graphs && bw == t) {
             auto it = graph.find(t);
@@ -416,6 +416,7 @@ struct Engine {
             TRY(launch_all(t, prefill, bw));
         }
         if (nwant == 0) return 0;
+        if (out_tok) return tsl_download(out_tok, next.p, nwant * 4);
         return tsl_download(out, logits.p, nwant * (size_t)cfg.vocab * 4);
     }
 };
@@ -622,15 +623,17 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
                 }
                 last.push_back((int32_t)toks.size() - 1);
             }
-            std::vector<float> logits(last.size() * (size_t)vocab);
+            // The next tokens come from the GPU's argmax (fused/argmax, the
+            // same first-largest rule as argmax here), not from the logits.
+            std::vector<int32_t> next(last.size());
             int mode = admit.size() == 1 ? PREFILL : PACKED;
             TRY(e->step(toks.size(), toks.data(), pos.data(), slots.data(), mode, starts.data(), 0, nullptr, nullptr,
-                        last.size(), last.data(), logits.data()));
+                        last.size(), last.data(), nullptr, next.data()));
             st.prefill_steps++;
             st.prompt_tokens += toks.size();
             for (size_t i = 0; i < admit.size(); i++) {
                 int id = admit[i].first;
-                int32_t t = (int32_t)argmax(&logits[i * vocab], vocab);
+                int32_t t = next[i];
                 emit(id, t);
                 size_t plen = (size_t)(offsets[id + 1] - offsets[id]);
                 Seq s{id, admit[i].second, plen, t, max_new[id] - 1};
@@ -656,16 +659,16 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
             lens.push_back((int32_t)s.len + 1);
             want.push_back((int32_t)b);
         }
-        std::vector<float> logits(nb * (size_t)vocab);
+        std::vector<int32_t> next(nb);
         TRY(e->step(nb, toks.data(), pos.data(), slots.data(), DECODE, nullptr, nb, tables.data(), lens.data(), nb,
-                    want.data(), logits.data()));
+                    want.data(), nullptr, next.data()));
         st.decode_steps++;
         st.largest_batch = std::max<int64_t>(st.largest_batch, nb);
         st.decode_tokens += nb;
         std::vector<Seq> keep;
         for (size_t b = 0; b < nb; b++) {
             Seq s = running[b];
-            int32_t t = (int32_t)argmax(&logits[b * vocab], vocab);
+            int32_t t = next[b];
             s.len++;
             s.last = t;
             s.left--;

@@ -8,6 +8,8 @@
 // than the register budget take a second, cache-resident pass.
 #include "common.h"
 
+#include <climits>
+
 namespace {
 
 constexpr int ROWS_PER_WG = 4;  // one wavefront per row, 4 per workgroup
@@ -445,6 +447,62 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a, long nq, long nkv
     }
 }
 
+// ---------------------------------------------------------------- argmax
+// out[r] = argmax (src/llm/mod.rs:132-140) of row r of X [B, V]: the index
+// the sequential scan `if x[i] > x[best] { best = i }` ends on. So a NaN at
+// index 0 is the answer (nothing compares greater), later NaNs never are,
+// and otherwise it is the first index of the largest value (+0 and -0 tie).
+// A workgroup per row: each thread scans its float4 chunks in ascending
+// order, then (value, index) pairs meet in a tree that keeps the larger
+// value, the lower index on ties.
+// Keeps the better of (bv, bi) and (v, i): i == INT_MAX is no candidate;
+// candidates are never NaN.
+TSL_DEV void am_pick(float& bv, int& bi, float v, int i) {
+    if (i == INT_MAX) return;
+    if (bi == INT_MAX || v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ X, int V, int* __restrict__ out) {
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    const int tid = threadIdx.x;
+    const float* x = X + (size_t)blockIdx.x * V;
+    float bv = 0.0f;
+    int bi = INT_MAX;  // no candidate yet
+    auto see = [&](float v, int i) {
+        if (v == v && (bi == INT_MAX || v > bv)) {  // ascending i: strict > keeps the first
+            bv = v;
+            bi = i;
+        }
+    };
+    if ((V & 3) == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0) {
+        for (int c = tid; 4 * c < V; c += 256) {
+            const float4v q = *reinterpret_cast<const float4v*>(x + 4 * c);
+            for (int e = 0; e < 4; e++) see(q[e], 4 * c + e);
+        }
+    } else {
+        for (int c = tid; c < V; c += 256) see(x[c], c);
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        am_pick(bv, bi, ov, oi);
+    }
+    if ((tid & 63) == 0) {
+        rv[tid >> 6] = bv;
+        ri[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; w++) am_pick(bv, bi, rv[w], ri[w]);
+        const float x0 = x[0];
+        out[blockIdx.x] = (x0 != x0 || bi == INT_MAX) ? 0 : bi;
+    }
+}
+
 int grid1(long n) {
     long g = (n + 255) / 256;
     return (int)(g < 1 ? 1 : (g > 65535 * 4 ? 65535 * 4 : g));
@@ -534,6 +592,15 @@ int launch_rmsnorm_rows(TslKernel& k, const uint64_t* a, hipStream_t s) {
     int ncols = (int)std::min<int64_t>(k.metav("BC"), Dm);
     return run_rmsnorm<float>(P<float>(a[0]), P<int>(a[1]), T, P<u16>(a[2]), P<u16>(a[3]), B, Dm, ncols,
                               arg_f32(a[4]), s, "rmsnorm_rows");
+}
+
+// fused/argmax (the engine's scheduler, not a .tl kernel): X [B, V] -> T [B].
+int launch_argmax(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    const int B = k.dim("B"), V = k.dim("V");
+    if (B == 0) return 0;
+    if (V == 0) return tsl_fail(-2, "argmax: rows of 0 values");
+    hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, s, P<float>(a[0]), V, P<int>(a[1]));
+    return TSL_LAUNCHED("argmax");
 }
 
 int launch_rope_q(TslKernel& k, const uint64_t* a, hipStream_t s) {

@@ -43,6 +43,7 @@ int launch_kv_write(TslKernel&, const uint64_t*, hipStream_t);
 int launch_rope_kv(TslKernel&, const uint64_t*, hipStream_t);
 int launch_linear_residual_rmsnorm(TslKernel&, const uint64_t*, hipStream_t);
 int launch_qkv_rope_kv(TslKernel&, const uint64_t*, hipStream_t);
+int launch_argmax(TslKernel&, const uint64_t*, hipStream_t);
 int launch_flash_attention(TslKernel&, const uint64_t*, hipStream_t);
 int launch_prefill_attention(TslKernel&, const uint64_t*, hipStream_t);
 int launch_decode_attention(TslKernel&, const uint64_t*, hipStream_t);
@@ -142,6 +143,9 @@ std::vector<KernelDef> g_defs = {
      "X: f16[T, Dm], Wqkv: f16[W, Dm], QKV: f16[T, W], pos: i32[T], slot: i32[T], C: f32[NPOS, D2], "
      "S: f32[NPOS, D2], Q: f16[T, H, D], Kc: f16[NS, G, D], Vc: f16[NS, G, D], K: f16[T, G, D], V: f16[T, G, D]",
      "", "D2 D", launch_qkv_rope_kv, prepare_projection},
+    // Not a .tl kernel: argmax of each row (src/llm/mod.rs:132-140), so the
+    // scheduler reads back token ids instead of logits.
+    {"fused", "argmax", "X: f32[B, V], T: i32[B]", "", "", launch_argmax, nullptr},
     {"llm", "prefill_attention",
      "Q: f16[S, H, D], K: f16[S, G, D], V: f16[S, G, D], starts: i32[S], O: f16[S, H, D], scale: f32",
      "BM = 64, BN = 64", "D", launch_prefill_attention, prepare_attention},

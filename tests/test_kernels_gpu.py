@@ -417,6 +417,32 @@ def test_fused_linear_residual_rmsnorm(m, k, n, mode):
         np.testing.assert_array_equal(out[4].view(np.uint16), py.view(np.uint16))
 
 
+def test_argmax_rows_vs_the_sequential_scan():
+    # fused/argmax (the scheduler's next token) against src/llm/mod.rs:132-140
+    # restated (oracle.argmax): first index of the largest value under `>`,
+    # a NaN at index 0 wins, later NaNs never do, +0 and -0 tie.
+    _say("argmax rows")
+    rng = np.random.default_rng(9)
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    rows = [np.array([1, 3, 3, 2], np.float32), np.array([nan, 5, 7], np.float32),
+            np.array([2, nan, 7, nan, 7], np.float32), np.array([-0.0, 0.0, -0.0], np.float32),
+            np.array([0.0, -0.0], np.float32), np.array([-inf, -inf, -inf], np.float32),
+            np.array([1, nan, nan, nan], np.float32), np.array([-1, -2, inf, inf], np.float32),
+            np.array([5], np.float32)]
+    for v in (4, 37, 1000, 32000, 32003):
+        rows.append(rng.integers(0, 6, v).astype(np.float32))  # many ties
+        x = rng.standard_normal(v).astype(np.float32)
+        x[rng.integers(0, v, 3)] = nan
+        rows.append(x)
+        rows.append(np.full(v, -inf, np.float32))
+    for r in rows:
+        for b in (1, 3):  # several rows of the same values at once
+            x = np.tile(r, (b, 1))
+            got = T.run("fused", "argmax", [x, np.zeros(b, np.int32)], outputs=[1])[1]
+            want = oracle.argmax(r)
+            assert (got == want).all(), (r[:8], got, want)
+
+
 @pytest.mark.parametrize("cfgname,t", [("tinyllama", 1), ("tinyllama", 32), ("tinyllama", 40), ("tinyllama", 64),
                                        ("tinyllama", 80), ("tiny", 16)])
 def test_fused_qkv_rope_kv(cfgname, t):
