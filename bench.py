@@ -13,7 +13,7 @@ events on the library's stream, bracketed by stream synchronisation.
   cases         the other BASELINE configs measured the same way: GEMM
                 1024^3/2048^3, causal FlashAttention H32 D64 S 512..4096,
                 paged GQA decode (GB/s against 8 TB/s), RMSNorm and softmax
-                4096^2, and (--llm) TinyLlama-shape decode tokens/s.
+                4096^2, and TinyLlama-shape decode tokens/s (skip with --no-llm).
 """
 
 import argparse
@@ -174,14 +174,14 @@ def rows_case(T, kind):
     return Timed(T, k, bufs), 4.0 * r * c
 
 
-def llm_case(T, seqs=32, prompt=512, new=128):
+def llm_case(T, seqs=32, prompt=512, new=128, graphs=True):
     """TinyLlama-1.1B shape, random fp16 weights, 32
     prompts of 512 random ids, 128 greedy steps under continuous batching."""
     cfg = T.Config.tinyllama()
     t0 = time.perf_counter()
     w = T.weights_random(cfg, 7)
     lim = T.Limits(16, seqs * ((prompt + new + 15) // 16) + 64, 1024, (prompt + new + 15) // 16)
-    e = T.Engine(cfg, lim, w)
+    e = T.Engine(cfg, lim, w, graphs=graphs)
     del w
     rng = np.random.default_rng(5)
     reqs = [(rng.integers(3, cfg.vocab, prompt).tolist(), new) for _ in range(seqs)]
@@ -207,7 +207,10 @@ def main():
     ap.add_argument("--no-cases", action="store_true", help="only the headline GEMM")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--llm", action="store_true", help="also run the TinyLlama decode case (config 5)")
+    ap.add_argument("--llm", action="store_true", help="(default) run the TinyLlama decode case (config 5)")
+    ap.add_argument("--no-llm", action="store_true", help="skip the TinyLlama decode case")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="TinyLlama case: launch decode steps kernel by kernel (for kernel traces)")
     ap.add_argument("--only", default="", help="comma list of cases: gemm1024,gemm2048,fa512..fa4096,decode,"
                     "rmsnorm,softmax,llm,copy (counter calibration); 'none' for the headline GEMM alone")
     ap.add_argument("--profile", action="store_true",
@@ -300,8 +303,8 @@ def main():
             m = t.median(50)
             cases.append({"case": f"{kind} 4096x4096", "ms": round(m, 5), "gbps": round(nb / m / 1e6, 1),
                           "frac_hbm": round(nb / m / 1e6 / PEAK_HBM, 4)})
-        if args.llm and want("llm"):
-            cases.append(llm_case(T))
+        if not args.no_llm and want("llm"):
+            cases.append(llm_case(T, graphs=not args.no_graphs))
     if cases:
         line["cases"] = cases
     if not args.no_cpu:

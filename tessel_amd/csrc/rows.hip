@@ -452,9 +452,10 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a, long nq, long nkv
 // the sequential scan `if x[i] > x[best] { best = i }` ends on. So a NaN at
 // index 0 is the answer (nothing compares greater), later NaNs never are,
 // and otherwise it is the first index of the largest value (+0 and -0 tie).
-// A workgroup per row: each thread scans its float4 chunks in ascending
-// order, then (value, index) pairs meet in a tree that keeps the larger
-// value, the lower index on ties.
+// A workgroup per row (1024 threads, 8 loads in flight each): each thread
+// scans its float4 chunks in ascending order, then (value, index) pairs
+// meet in a tree that keeps the larger value, the lower index on ties.
+
 // Keeps the better of (bv, bi) and (v, i): i == INT_MAX is no candidate;
 // candidates are never NaN.
 TSL_DEV void am_pick(float& bv, int& bi, float v, int i) {
@@ -465,9 +466,11 @@ TSL_DEV void am_pick(float& bv, int& bi, float v, int i) {
     }
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ X, int V, int* __restrict__ out) {
-    __shared__ float rv[4];
-    __shared__ int ri[4];
+constexpr int AM_THREADS = 1024, AM_UNROLL = 8;  // a 32000-float row in one round of loads
+__global__ __launch_bounds__(AM_THREADS) void argmax_kernel(const float* __restrict__ X, int V, int* __restrict__ out) {
+    constexpr int NW = AM_THREADS / 64;
+    __shared__ float rv[NW];
+    __shared__ int ri[NW];
     const int tid = threadIdx.x;
     const float* x = X + (size_t)blockIdx.x * V;
     float bv = 0.0f;
@@ -479,12 +482,23 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ X
         }
     };
     if ((V & 3) == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0) {
-        for (int c = tid; 4 * c < V; c += 256) {
-            const float4v q = *reinterpret_cast<const float4v*>(x + 4 * c);
-            for (int e = 0; e < 4; e++) see(q[e], 4 * c + e);
+        const int nc = V / 4;
+        for (int c0 = tid; c0 < nc; c0 += AM_THREADS * AM_UNROLL) {
+            float4v q[AM_UNROLL];
+#pragma unroll
+            for (int u = 0; u < AM_UNROLL; u++) {
+                const int c = c0 + u * AM_THREADS;
+                q[u] = c < nc ? *reinterpret_cast<const float4v*>(x + 4 * c) : float4v{};
+            }
+#pragma unroll
+            for (int u = 0; u < AM_UNROLL; u++) {
+                const int c = c0 + u * AM_THREADS;
+                if (c < nc)
+                    for (int e = 0; e < 4; e++) see(q[u][e], 4 * c + e);
+            }
         }
     } else {
-        for (int c = tid; c < V; c += 256) see(x[c], c);
+        for (int c = tid; c < V; c += AM_THREADS) see(x[c], c);
     }
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, 64);
@@ -497,7 +511,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ X
     }
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 4; w++) am_pick(bv, bi, rv[w], ri[w]);
+        for (int w = 1; w < NW; w++) am_pick(bv, bi, rv[w], ri[w]);
         const float x0 = x[0];
         out[blockIdx.x] = (x0 != x0 || bi == INT_MAX) ? 0 : bi;
     }
@@ -599,7 +613,7 @@ int launch_argmax(TslKernel& k, const uint64_t* a, hipStream_t s) {
     const int B = k.dim("B"), V = k.dim("V");
     if (B == 0) return 0;
     if (V == 0) return tsl_fail(-2, "argmax: rows of 0 values");
-    hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, s, P<float>(a[0]), V, P<int>(a[1]));
+    hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(AM_THREADS), 0, s, P<float>(a[0]), V, P<int>(a[1]));
     return TSL_LAUNCHED("argmax");
 }
 
