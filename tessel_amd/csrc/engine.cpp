@@ -517,9 +517,9 @@ int tsl_engine_free(int engine) {
     Engine* e = get(engine);
     if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
     tsl_sync();
+    // (tok, pos, slot, idx, starts, lens and table are views into `in`.)
     Buf* bufs[] = {&e->embed, &e->norm, &e->cos, &e->sin, &e->x, &e->h, &e->qkv, &e->q, &e->k, &e->v,
-                   &e->o, &e->mlp, &e->last, &e->logits, &e->tok, &e->pos, &e->slot, &e->idx, &e->table,
-                   &e->lens, &e->starts};
+                   &e->o, &e->mlp, &e->last, &e->logits, &e->in, &e->next};
     if (e->head.p != e->embed.p) tsl_free(e->head.p);
     for (Buf* b : bufs)
         if (b->p) tsl_free(b->p);

@@ -246,6 +246,9 @@ int tsl_fail(int code, const std::string& msg) {
 
 int tsl_hip_check(hipError_t e, const char* what) {
     if (e == hipSuccess) return 0;
+    // Reported here, so clear HIP's last-error state: a later, unrelated
+    // launch check (hipGetLastError) must not report this call again.
+    (void)hipGetLastError();
     std::ostringstream o;
     o << what << ": HIP error " << (int)e << " " << hipGetErrorName(e) << " (" << hipGetErrorString(e) << ")";
     return tsl_fail(TSL_ERR_HIP, o.str());

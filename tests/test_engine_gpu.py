@@ -107,3 +107,17 @@ def test_engine_from_a_bf16_checkpoint(gpu, tmp_path):
     print(f"bf16 checkpoint prefill: logits within {err:.2e} of the reference", flush=True)
     assert err < 2e-2
     e.close()
+
+
+def test_close_then_launch():
+    # Closing an engine frees exactly its own allocations (its step inputs
+    # are views into one arena): a kernel launched afterwards reports no
+    # error left behind by the close.
+    cfg = T.Config.tiny()
+    w = T.weights_random(cfg, 4)
+    e = T.Engine(cfg, T.Limits(16, 64, 64, 8), w)
+    e.generate([([1, 2, 3], 3)], 1)
+    e.close()
+    a = np.ones((64, 64), np.float16)
+    c = T.run("matmul", "matmul", [a, a, np.zeros((64, 64), np.float16)], outputs=[2])[2]
+    assert (c == 64).all()
