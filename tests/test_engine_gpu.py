@@ -49,6 +49,36 @@ def test_prefill_and_batched_decode_match_the_reference(gpu):
     e.close()
 
 
+def test_wide_model_shape_against_the_reference(gpu):
+    # A Llama-7B-wide shape (dim 4096, head_dim 128, GQA 32/8, ffn 11008),
+    # two layers and a small vocabulary: projections with K > 2048 (split
+    # QKV without the fused rotation, split gate_up, down at K = 11008), the
+    # 4096-column reduce-and-normalise, and decode attention at D = 128.
+    vals = (4096, 2, 32, 8, 128, 11008, 4000, 1e-5, 10000.0, 512, 1, 2)
+    cfg, ocfg = T.Config(*vals), oracle.Config(*vals)
+    w = T.weights_random(cfg, 21)
+    e = T.Engine(cfg, limits(page=16, pages=16, max_tokens=32, max_seq_pages=4), w)
+    prompt = [1, 17, 200, 33, 5, 99, 64, 3, 250, 12, 3000, 7]
+    n = len(prompt)
+    got = e.step(prompt, list(range(n)), list(range(n)), T.Engine.PREFILL, want=[n - 1])
+    want = oracle.forward(ocfg, w, prompt)
+    err = rel(got[0], want[n - 1])
+    print(f"wide prefill: logits within {err:.2e} of the reference", flush=True)
+    assert err < 2e-2
+    reqs = [(prompt, 3), ([1, 2, 3, 4, 5], 3)]
+    outs, st = e.generate(reqs, 2)
+    e.close()
+    assert st.largest_batch == 2
+    for (p, m), toks in zip(reqs, outs):
+        assert len(toks) == m
+        seq = list(p)
+        for t in toks:
+            l = oracle.forward(ocfg, w, seq)[-1]
+            best = oracle.argmax(l)
+            assert t == best or l[best] - l[t] < 2e-2 * np.abs(l).max(), (t, best)
+            seq.append(t)
+
+
 def test_packed_prefill_matches_one_prompt_per_step(gpu):
     cfg = T.Config.tiny()
     w = T.weights_random(cfg, 11)
