@@ -1288,7 +1288,9 @@ int launch_gate_up(TslKernel& k, const uint64_t* a, hipStream_t s) {
 // X [M, K], W [N, K], R [M, N], Wn [N], Y [M, N], eps. Few-row products run
 // K-split (at least 2 slices) and one kernel adds the slices to R and
 // normalises each row; with the slice count linear_residual would use, the
-// bits are that pair's. Other shapes launch the pair.
+// bits are that pair's. Prefill-sized products that linear_residual
+// splits over K (128 x 128 tiles) end in the same kernel, with the pair's
+// bits too; other shapes launch the pair.
 SkPlan fused_plan(int M, int N, int K, int ncols) {
     SkPlan p = sk_plan(true, M, N, K);
     if (!p.use || ncols != N || !reduce_rmsnorm_fits(N)) return SkPlan{};
@@ -1307,6 +1309,20 @@ int launch_linear_residual_rmsnorm(TslKernel& k, const uint64_t* a, hipStream_t 
         float* part = reinterpret_cast<float*>(k.scratch);
         launch_skinny_m<EPI_RESID>(P<u16>(a[0]), P<u16>(a[1]), nullptr, R, nullptr, M, N, K, p, part, s, false);
         return run_reduce_rmsnorm(part, p.split, R, P<u16>(a[3]), P<u16>(a[4]), M, N, eps, s);
+    }
+    // Prefill-sized products that linear_residual splits over K (128 x 128
+    // tiles, big_split) feed the same reduce-and-normalise kernel.
+    const bool aligned = K % 8 == 0 && (long)M * K < (1L << 30) && (long)N * K < (1L << 30);
+    const long tiles256 = (long)((M + 255) / 256) * ((N + 255) / 256);
+    const int bsplit = k.scratch && aligned && M > 64 && tiles256 < 224 ? big_split(M, N, K) : 1;
+    if (bsplit > 1 && ncols == N && reduce_rmsnorm_fits(N)) {
+        const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
+        hipLaunchKernelGGL((gemm_big<true, EPI_RESID, 128, 128, 2, 2, 64, 2, true>), dim3(tiles, bsplit), dim3(256), 0, s,
+                           P<u16>(a[0]), P<u16>(a[1]), nullptr, R, nullptr, M, N, K, 4,
+                           reinterpret_cast<float*>(k.scratch));
+        if (int e = TSL_LAUNCHED("linear_residual_rmsnorm")) return e;
+        return run_reduce_rmsnorm(reinterpret_cast<float*>(k.scratch), bsplit, R, P<u16>(a[3]), P<u16>(a[4]), M, N, eps,
+                                  s);
     }
     if (int e = gemm_dispatch<true, EPI_RESID>(P<u16>(a[0]), P<u16>(a[1]), nullptr, R, nullptr, M, N, K, s,
                                                "linear_residual_rmsnorm", reinterpret_cast<float*>(k.scratch)))

@@ -389,11 +389,12 @@ def test_llm_rows(t, dm):
 
 @pytest.mark.parametrize("m,k,n,mode", [(32, 5632, 2048, "split"), (32, 2048, 2048, "own split"),
                                         (5, 1024, 1000, "own split"), (7, 4160, 33, "pair"), (128, 2048, 2048, "pair"),
-                                        (200, 4160, 300, "pair")])
+                                        (200, 4160, 300, "pair"), (512, 5632, 2048, "pair")])
 def test_fused_linear_residual_rmsnorm(m, k, n, mode):
     # The engine's fused launch (fused/linear_residual_rmsnorm): R += X W^T,
     # then Y = rmsnorm(R) Wn, against the oracle and against llm/linear_residual
-    # followed by llm/rmsnorm. "pair": the shape launches exactly that pair.
+    # followed by llm/rmsnorm. "pair": bits of exactly that pair (prefill
+    # shapes split over K end in the reduce-and-normalise kernel too).
     # "split": K is split as linear_residual splits it, so R and Y have the
     # pair's bits too. "own split": a split linear_residual does not make, so
     # R and Y are within the float tolerance.
