@@ -868,7 +868,10 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         }
         if (u + XD < mysteps) load_x(st + SK_WAVES * XD, slot);
     }
-    if (mysteps == 0) __syncthreads();  // matches the barrier of wavefronts with steps
+    if (mysteps == 0) {  // no k step here, but a share of the W loads: land them, then the barrier
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        __syncthreads();
+    }
     // Sum the 8 partial tiles through LDS in wavefront order; thread tid < 256
     // keeps element tid (register tid/64 of lane tid%64) of each.
     float sum[MT];

@@ -128,12 +128,14 @@ def test_llm_matmuls_tinyllama_shapes(name, m):
 
 @pytest.mark.parametrize("name", MM_CASES)
 @pytest.mark.parametrize("m,k,n", [(40, 192, 100), (7, 4160, 33), (64, 64, 1), (40, 2176, 100), (3, 384, 17),
-                                   (17, 4352, 50), (32, 2048, 5000), (20, 1024, 4500)])
+                                   (17, 4352, 50), (32, 2048, 5000), (20, 1024, 4500), (5, 128, 40), (9, 256, 70)])
 def test_llm_matmuls_ragged_few_rows(name, m, k, n):
     # Few-row (decode-sized) products with ragged M and N, one K step, a long
     # K that is split across workgroups, and (K % 128 == 0) the LDS-staged
     # blocks with uneven K slices and a partial last block of rows; more
-    # blocks than CUs at K = 1024 or 2048 take the persistent form.
+    # blocks than CUs at K = 1024 or 2048 take the persistent form. K = 128,
+    # 256 and 384 leave wavefronts without a k step of their own (they still
+    # load a share of the block).
     _say("llm mm ragged", name, m, k, n)
     r = oracle.Rng(300 + m + n)
     args, want = _mm_args(r, name, m, k, n, wscale=1.0 / np.sqrt(k))
@@ -388,6 +390,7 @@ def test_llm_rows(t, dm):
 
 
 @pytest.mark.parametrize("m,k,n,mode", [(32, 5632, 2048, "split"), (32, 2048, 2048, "own split"),
+                                        (7, 4160, 36, "split"), (40, 11008, 4096, "split"),
                                         (5, 1024, 1000, "own split"), (7, 4160, 33, "pair"), (128, 2048, 2048, "pair"),
                                         (200, 4160, 300, "pair"), (512, 5632, 2048, "pair")])
 def test_fused_linear_residual_rmsnorm(m, k, n, mode):
