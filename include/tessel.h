@@ -140,6 +140,15 @@ int tsl_engine_free(int engine);
 /* Engine flags: graphs (decode-step graph replay), tune (matmul tuner). */
 int tsl_engine_set(int engine, int graphs, int tune);
 
+/* Gpu::profile for the engine's launches (src/gpu.rs:40, :197-228): on != 0
+ * clears the profile and times every launch on its own (graphs are not
+ * replayed meanwhile); rows: the profile as JSON text, a list of {"phase":
+ * "prefill"|"decode", "kernel": "{name} -> {output shape}", "launches": n,
+ * "ms": total}, largest time first. *len gets the text's length; out gets
+ * the text (NUL-terminated) when cap > *len. */
+int tsl_engine_profile(int engine, int on);
+int tsl_engine_profile_rows(int engine, char* out, size_t cap, size_t* len);
+
 /* Engine::step (src/llm/engine.rs:275-354). mode 0 = Prefill, 1 = Packed
  * (starts[n]), 2 = Decode (tables: nseq rows of max_seq_pages pages, lens:
  * nseq). logits receives nwant * vocab floats for rows want[0..nwant). */

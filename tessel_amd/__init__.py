@@ -9,6 +9,7 @@ fallback: without the library every call raises.
 """
 
 import ctypes
+import json
 import os
 import struct
 
@@ -47,7 +48,7 @@ EXPORTS = [
     "tsl_event_elapsed", "tsl_weights_sizes", "tsl_weights_random", "tsl_engine_new", "tsl_engine_free",
     "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
     "tsl_checkpoint_save", "tsl_json_roundtrip", "tsl_rng_new", "tsl_rng_bits", "tsl_rng_tensor",
-    "tsl_time_each",
+    "tsl_time_each", "tsl_engine_profile", "tsl_engine_profile_rows",
 ]
 
 
@@ -116,6 +117,8 @@ def _declare(L):
     L.tsl_checkpoint_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config), _P, _P, _P, _P, ctypes.POINTER(_INT)]
     L.tsl_checkpoint_save.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config), _P, _P, _P, _P]
     L.tsl_json_roundtrip.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    L.tsl_engine_profile.argtypes = [_INT, _INT]
+    L.tsl_engine_profile_rows.argtypes = [_INT, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
     L.tsl_time_each.argtypes = [_INT, ctypes.POINTER(_U64), _INT, _INT, _P]
     L.tsl_rng_new.argtypes = [_U64, ctypes.POINTER(_U64)]
     L.tsl_rng_bits.argtypes = [ctypes.POINTER(_U64), ctypes.POINTER(_U64)]
@@ -441,6 +444,18 @@ class Engine:
                                     ln.ctypes.data if ln is not None else None, want.size,
                                     want.ctypes.data if want.size else None, out.ctypes.data))
         return out
+
+    def profile(self, on):
+        """Gpu::profile: time every launch on its own (graphs off) from now."""
+        check(lib().tsl_engine_profile(self.handle, int(bool(on))))
+
+    def profile_rows(self):
+        """[(phase, kernel, launches, ms)], largest time first."""
+        n = ctypes.c_size_t()
+        check(lib().tsl_engine_profile_rows(self.handle, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(n.value + 1)
+        check(lib().tsl_engine_profile_rows(self.handle, buf, n.value + 1, ctypes.byref(n)))
+        return [(r["phase"], r["kernel"], r["launches"], r["ms"]) for r in json.loads(buf.value.decode())]
 
     def generate(self, requests, max_batch, packed=True):
         """sched::generate_with: requests = [(prompt tokens, max_new)] ->

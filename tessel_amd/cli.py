@@ -10,10 +10,10 @@ these unchanged.
     python -m tessel_amd llm-tiny DIR
 
 Differences, all stated in the output or the usage text: the device is
-"Hip" (there is no CPU emulator: `--device emu` is refused), `sm_mhz` is
-null (no clock query), and `llm --profile` is refused. The code generators
-(ir, cuda, metal, pallas) and `run` (which checks against the interpreter)
-are not part of this library.
+"Hip" (there is no CPU emulator: `--device emu` is refused) and `sm_mhz`
+is null (no clock query). The code generators (ir, cuda, metal, pallas)
+and `run` (which checks against the interpreter) are not part of this
+library.
 """
 
 import json
@@ -38,6 +38,7 @@ usage:
              [--logits OUT]  (also writes the logits after the first prompt, as JSON)
              [--no-graphs]   (launch every decode step's kernels one by one, not as a HIP graph)
              [--no-tune]     (default matmul tiles instead of tuning them on the GPU)
+             [--profile]     (then runs it all once more timing every kernel launch: time by kernel)
              [--no-pack]     (each new prompt in a prefill step of its own, not packed together)
                (greedy generation with the engine of tessel kernels, continuous
                batching over a paged KV cache; MODEL_DIR is a Hugging Face Llama
@@ -315,8 +316,6 @@ def llm(args):
     dev = flag(args, "--device") or "hip"
     if dev not in ("hip", "cuda"):
         raise CliError(f"unknown device {dev}" + (" (this library has no CPU emulator)" if dev == "emu" else ""))
-    if "--profile" in args:
-        raise CliError("--profile is not supported by this library (time kernels with rocprofv3 instead)")
     path = flag(args, "--prompts")
     if path is None:
         raise CliError("--prompts is required")
@@ -362,6 +361,23 @@ def llm(args):
             warm_s = time.perf_counter() - t0
         outs, st = e.generate(reqs, batch, pack)
         ttft = e.first_token_s
+        # The same work once more with every launch timed on its own (and
+        # without graphs), after the timed run so it does not change it.
+        prof = ""
+        if "--profile" in args:
+            e.profile(True)
+            e.generate(reqs, batch, pack)
+            rows = e.profile_rows()
+            e.profile(False)
+            total = sum(ms for ph, _, _, ms in rows if ph == "decode")
+            print(f"decode, kernel time by kernel ({total:.1f} ms in all, launched one at a time):", file=sys.stderr)
+            items = []
+            for ph, kn, n, ms in rows:
+                if ph == "decode":
+                    print(f"  {100.0 * ms / max(total, 1e-9):>5.1f}%  {ms:>9.2f} ms  {n:>6}x  {kn}", file=sys.stderr)
+                items.append(f'{{"phase": "{ph}", "kernel": "{kn.replace(chr(34), chr(39))}", "launches": {n}, '
+                             f'"ms": {ms:.3f}}}')
+            prof = ', "profile": [' + ", ".join(items) + "]"
     finally:
         e.close()
     ids = ", ".join("[" + ", ".join(str(t) for t in o) + "]" for o in outs)
@@ -373,7 +389,7 @@ def llm(args):
             f'"largest_batch": {st.largest_batch}, "graphs": {"true" if graphs else "false"}, '
             f'"packed": {"true" if pack else "false"}, "load_s": {load_s:.2f}, "upload_s": {upload_s:.2f}, '
             f'"warmup_s": {warm_s:.2f}, "first_token_s": [{", ".join(f"{x:.4f}" for x in ttft)}], '
-            f'"outputs": [{ids}]}}')
+            f'"outputs": [{ids}]{prof}}}')
     print(line, flush=True)
     jp = flag(args, "--json")
     if jp is not None:

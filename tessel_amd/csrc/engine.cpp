@@ -120,6 +120,12 @@ struct Engine {
     tsl_config cfg;
     tsl_limits lim;
     bool graphs = true, tune = true;
+    // Gpu::profile (src/gpu.rs:40, :197-217): when on, every launch is timed
+    // on its own and summed per (phase, "{name} -> {output shape}").
+    bool profiling = false;
+    const char* phase = "decode";
+    std::map<std::pair<std::string, std::string>, std::pair<int64_t, double>> prof;
+    std::map<int, std::string> kname;
     std::map<size_t, int> graph;
     std::map<std::string, int> tuned;
     Buf embed, head, norm, cos, sin;
@@ -169,14 +175,29 @@ struct Engine {
             names.push_back(m.first.c_str());
             vals.push_back(m.second);
         }
-        return tsl_kernel(file, name, (int)shapes.size(), ranks.data(), dims.data(), (int)meta.size(), names.data(),
-                          vals.data(), warps, handle);
+        int r = tsl_kernel(file, name, (int)shapes.size(), ranks.data(), dims.data(), (int)meta.size(), names.data(),
+                           vals.data(), warps, handle);
+        if (r == 0 && !kname.count(*handle)) {  // src/gpu.rs:168-169
+            std::ostringstream o;
+            o << name << " -> [";
+            const auto& last = shapes.back();
+            for (size_t i = 0; i < last.size(); i++) o << (i ? ", " : "") << last[i];
+            o << "]";
+            kname[*handle] = o.str();
+        }
+        return r;
     }
 
     int launch(int k, const std::vector<Arg>& args) {
         std::vector<uint64_t> raw;
         for (auto& a : args) raw.push_back(a.v);
-        return tsl_launch(k, raw.data(), (int)raw.size());
+        if (!profiling) return tsl_launch(k, raw.data(), (int)raw.size());
+        float ms = 0.0f;
+        TRY(tsl_time_each(k, raw.data(), (int)raw.size(), 1, &ms));
+        auto& e = prof[{phase, kname[k]}];
+        e.first += 1;
+        e.second += ms;
+        return 0;
     }
 
     // Engine::mm (src/llm/engine.rs:233-270): with tuning on, every
@@ -397,7 +418,9 @@ struct Engine {
         }
         TRY(write(in, 0, hin.data(), nin * 4));
         bool prefill = mode != DECODE;
-        if (!prefill && graphs && bw == t) {
+        phase = prefill ? "prefill" : "decode";
+        // Profiling times every launch on its own, so it runs without graphs.
+        if (!prefill && graphs && !profiling && bw == t) {
             auto it = graph.find(t);
             if (it != graph.end()) {
                 TRY(tsl_replay(it->second));
@@ -526,6 +549,41 @@ int tsl_engine_free(int engine) {
     for (auto& L : e->layers)
         for (Buf* b : {&L.n1, &L.wqkv, &L.wo, &L.n2, &L.wg, &L.wu, &L.wd, &L.kc, &L.vc}) tsl_free(b->p);
     g_engines[engine].reset();
+    return 0;
+}
+
+// Gpu::profile on (cleared) or off, and profile_rows (src/gpu.rs:219-228):
+// the rows as a JSON list of {"phase", "kernel", "launches", "ms"}, largest
+// time first; *len gets its length, out the text when cap > *len.
+int tsl_engine_profile(int engine, int on) {
+    Engine* e = get(engine);
+    if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
+    e->profiling = on != 0;
+    e->prof.clear();
+    return 0;
+}
+int tsl_engine_profile_rows(int engine, char* out, size_t cap, size_t* len) {
+    Engine* e = get(engine);
+    if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
+    std::vector<std::pair<std::pair<std::string, std::string>, std::pair<int64_t, double>>> rows(e->prof.begin(),
+                                                                                                 e->prof.end());
+    std::stable_sort(rows.begin(), rows.end(),
+                     [](const auto& a, const auto& b) { return a.second.second > b.second.second; });
+    std::ostringstream o;
+    o << "[";
+    for (size_t i = 0; i < rows.size(); i++) {
+        std::string k = rows[i].first.second;
+        for (auto& c : k)
+            if (c == '"') c = '\'';
+        char ms[32];
+        std::snprintf(ms, sizeof ms, "%.6f", rows[i].second.second);
+        o << (i ? ", " : "") << "{\"phase\": \"" << rows[i].first.first << "\", \"kernel\": \"" << k
+          << "\", \"launches\": " << rows[i].second.first << ", \"ms\": " << ms << "}";
+    }
+    o << "]";
+    const std::string s = o.str();
+    if (len) *len = s.size();
+    if (out && cap > s.size()) std::memcpy(out, s.c_str(), s.size() + 1);
     return 0;
 }
 

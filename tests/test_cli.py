@@ -94,12 +94,18 @@ def test_llm_on_a_tiny_checkpoint(tmp_path):
     p = tmp_path / "p.json"
     p.write_text(json.dumps(prompts))
     r = _cli("llm", str(d), "--prompts", str(p), "--max-new", "6", "--batch", "2", "--warmup", "--json",
-             str(tmp_path / "o.json"), "--logits", str(tmp_path / "l.json"))
+             str(tmp_path / "o.json"), "--logits", str(tmp_path / "l.json"), "--profile")
     assert r.returncode == 0, r.stderr
     line = json.loads(r.stdout)
     assert line["engine"] == "tessel" and line["requests"] == 3 and line["batch"] == 2
     assert line["prompt_tokens"] == 12 and len(line["first_token_s"]) == 3
     assert json.loads((tmp_path / "o.json").read_text()) == line
+    # --profile: every launch of a third run timed, by phase and kernel.
+    prof = line["profile"]
+    assert {x["phase"] for x in prof} == {"prefill", "decode"}
+    assert any(x["kernel"].startswith("decode_attention -> [") for x in prof)
+    assert all(x["launches"] > 0 and x["ms"] > 0 for x in prof)
+    assert "decode, kernel time by kernel" in r.stderr
     # The same generation through the library.
     T.open()
     cfg, w = T.load_checkpoint(str(d))
