@@ -49,6 +49,16 @@ TSL_DEV half4 lds_read_tr(const void* p) {
     return __builtin_bit_cast(half4, v);
 }
 
+// x of lane l ^ 32, by v_permlane32_swap (registers only; a __shfl_xor
+// would round-trip through LDS with ds_bpermute). Swapping a copy of x with
+// itself leaves x[l + 32] in the source's lower half and x[l - 32] in the
+// destination's upper half.
+TSL_DEV float xor32(float x) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // LDS layouts of a 64-key block (K then V, each [64][D] row-major, 2D bytes
 // a row) with 16-byte-chunk XOR swizzles chosen so that the lane groups LDS
 // serves together (16 lanes of a 16-byte read, 32 of an 8-byte transposed
@@ -216,7 +226,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
             for (int r = 0; r < 16; r++) mb = fmaxf(mb, st[kt][r]);
-        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        mb = fmaxf(mb, xor32(mb));
         // Lazy rescaling: the running max moves only when it would grow by
         // more than 2^LAZY (p stays <= 2^LAZY meanwhile; acc / l does not
         // depend on which max was used).
@@ -260,7 +270,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
         }
     }
 
-    const float l = lsum + __shfl_xor(lsum, 32, 64);
+    const float l = lsum + xor32(lsum);
     if (myq < a.S) {
         u16* o = a.O + (long)myq * a.q_row + (long)h * a.q_head;
 #pragma unroll
