@@ -39,18 +39,6 @@ TSL_DEV void rope_rotate(float x1, float x2, float c, float s, u16& y1, u16& y2)
     y2 = f2h(__builtin_fmaf(x2, c, x1 * s));
 }
 
-// Largest / sum over the 64 lanes of a wavefront, every lane receiving it.
-TSL_DEV float wave_max(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-    return x;
-}
-TSL_DEV float wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
-}
-
 // DPP row operations within 16-lane rows (gfx9 DPP controls).
 template <int CTRL>
 TSL_DEV float dpp(float x) {
@@ -61,6 +49,29 @@ TSL_DEV float dpp(float x) {
 #define DPP_XOR2 0x4e
 #define DPP_HALF_MIRROR 0x141
 #define DPP_MIRROR 0x140
+
+TSL_DEV float lane_value(float x, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+// Largest / sum over the 64 lanes of a (fully active) wavefront, every lane
+// receiving it: four DPP steps within each 16-lane row (all of a row's lanes
+// then hold its result), then the four rows read out by readlane. Registers
+// only: a __shfl_xor butterfly would make six ds_bpermute round trips.
+TSL_DEV float wave_max(float x) {
+    x = fmaxf(x, dpp<DPP_XOR1>(x));
+    x = fmaxf(x, dpp<DPP_XOR2>(x));
+    x = fmaxf(x, dpp<DPP_HALF_MIRROR>(x));
+    x = fmaxf(x, dpp<DPP_MIRROR>(x));
+    return fmaxf(fmaxf(lane_value(x, 0), lane_value(x, 16)), fmaxf(lane_value(x, 32), lane_value(x, 48)));
+}
+TSL_DEV float wave_sum(float x) {
+    x += dpp<DPP_XOR1>(x);
+    x += dpp<DPP_XOR2>(x);
+    x += dpp<DPP_HALF_MIRROR>(x);
+    x += dpp<DPP_MIRROR>(x);
+    return (lane_value(x, 0) + lane_value(x, 16)) + (lane_value(x, 32) + lane_value(x, 48));
+}
 
 // A kernel specialised by tsl_kernel: its resolved dimensions and meta
 // values, in the order the .tl signature names them.
