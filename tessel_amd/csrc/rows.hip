@@ -500,11 +500,22 @@ __global__ __launch_bounds__(AM_THREADS) void argmax_kernel(const float* __restr
     } else {
         for (int c = tid; c < V; c += AM_THREADS) see(x[c], c);
     }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
+    // Within each 16-lane row by DPP (value and index moved together), then
+    // the four rows by readlane: registers only.
+    auto step = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        const float ov = dpp<C>(bv);
+        const int oi = __builtin_amdgcn_mov_dpp(bi, C, 0xf, 0xf, false);
         am_pick(bv, bi, ov, oi);
-    }
+    };
+    step(std::integral_constant<int, DPP_XOR1>{});
+    step(std::integral_constant<int, DPP_XOR2>{});
+    step(std::integral_constant<int, DPP_HALF_MIRROR>{});
+    step(std::integral_constant<int, DPP_MIRROR>{});
+    for (int r = 16; r < 64; r += 16)
+        am_pick(bv, bi, lane_value(bv, r), __builtin_amdgcn_readlane(bi, r));
+    bv = lane_value(bv, 0);  // rows 1..3 were folded into lane 0's pair; every lane takes it
+    bi = __builtin_amdgcn_readlane(bi, 0);
     if ((tid & 63) == 0) {
         rv[tid >> 6] = bv;
         ri[tid >> 6] = bi;
