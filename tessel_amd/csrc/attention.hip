@@ -49,16 +49,6 @@ TSL_DEV half4 lds_read_tr(const void* p) {
     return __builtin_bit_cast(half4, v);
 }
 
-// x of lane l ^ 32, by v_permlane32_swap (registers only; a __shfl_xor
-// would round-trip through LDS with ds_bpermute). Swapping a copy of x with
-// itself leaves x[l + 32] in the source's lower half and x[l - 32] in the
-// destination's upper half.
-TSL_DEV float xor32(float x) {
-    const uint32_t b = __builtin_bit_cast(uint32_t, x);
-    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
-    return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
-}
-
 // LDS layouts of a 64-key block (K then V, each [64][D] row-major, 2D bytes
 // a row) with 16-byte-chunk XOR swizzles chosen so that the lane groups LDS
 // serves together (16 lanes of a 16-byte read, 32 of an 8-byte transposed

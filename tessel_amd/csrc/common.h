@@ -50,6 +50,22 @@ TSL_DEV float dpp(float x) {
 #define DPP_HALF_MIRROR 0x141
 #define DPP_MIRROR 0x140
 
+// x of lane l ^ 32 / l ^ 16, by v_permlane32_swap / v_permlane16_swap
+// (registers only; a __shfl_xor would round-trip through LDS with
+// ds_bpermute). Swapping a copy of x with itself leaves the partner's value
+// in the source for the lower lanes of each pair and in the destination
+// for the upper ones.
+TSL_DEV float xor32(float x) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+TSL_DEV float xor16(float x) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+
 TSL_DEV float lane_value(float x, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
 }

@@ -392,8 +392,8 @@ __global__ __launch_bounds__(64 * NWV) void decode_tiles(DecArgs a) {
             x[r] = t0 + r < n ? sc[r] * a.c2 : -INFINITY;
             mb = fmaxf(mb, x[r]);
         }
-        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        mb = fmaxf(mb, xor16(mb));
+        mb = fmaxf(mb, xor32(mb));
         if (__builtin_amdgcn_ballot_w64(mb > m + LAZY) != 0) {
             const float mn = fmaxf(m, mb);
             const float alpha = __builtin_amdgcn_exp2f(m - mn);
@@ -421,8 +421,8 @@ __global__ __launch_bounds__(64 * NWV) void decode_tiles(DecArgs a) {
     }
 
     // Lane l holds head l%16, d = 16 dt + 4 (l/16) + r.
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
+    lsum += xor16(lsum);
+    lsum += xor32(lsum);
     // Merge the wavefronts' states in LDS (the rings are idle), in wave order.
     static_assert(NWV * QPG * (2 + D) * 4 <= NWV * DEC_STAGES * WSTAGE, "merge area exceeds the rings");
     float* red = reinterpret_cast<float*>(lds);  // [NWV][QPG][2 + D]
