@@ -3,8 +3,11 @@
 // (kernels/attention.tl:29-51, the same with G == H). HBM-bound.
 //
 // The .tl runs one program per (sequence b, query head h) and so reads each
-// KV page H/G times; here one workgroup owns (b, kv head g, chunk of CH
-// pages) and reads each page once for all QPG = H/G query heads sharing it.
+// KV page H/G times; here each page is read once for all QPG = H/G query
+// heads sharing it. Three forms: decode_stream (tables longer than 64 pages,
+// 4 or 8 kv heads: persistent workgroups over equal shares of all the
+// sequences' tiles), decode_tiles (matrix-core form; one workgroup per
+// (b, kv head g, chunk of CH pages)) and decode_partial (any D and P).
 // A token's D halves are spread over D/8 lanes (16-byte loads, 256
 // contiguous bytes per token at D = 128); every lane keeps its own online
 // softmax over the tokens it reads (log2 domain), and the states are merged
@@ -28,7 +31,8 @@ struct DecArgs {
     const u16 *Kc, *Vc;
     const int *table, *lens;
     u16* O;
-    float* part;  // [B][G][NCH][QPG][2 + D]: m, l, acc
+    float* part;  // [B][G][NCH][QPG][2 + D]: m, l, acc (stream path: range states, see DsGeom)
+    int* pre;     // stream path: first unit of each sequence, [B + 1]
     int B, H, G, NP, P, MP, NCH;
     int CH;  // pages per chunk
     int pshift;  // log2(P) (P is a power of two)
@@ -507,6 +511,494 @@ __global__ __launch_bounds__(256) void decode_merge(DecArgs a) {
     }
 }
 
+// ---- Balanced decode of long tables (decode_stream) ----
+// The work is the list of units (sequence b, 16-token tile j) over all kv
+// heads, j running through b's last page: U = sum_b ceil(lens_b / P) P / 16,
+// sequence-major. W persistent workgroups (one per CU) take equal contiguous
+// ranges [w U / W, (w + 1) U / W) of it, so every CU streams the same number
+// of bytes whatever the lengths, and no workgroup waits on a startup or a
+// tail of its own. Wavefront g of a workgroup computes kv head g, so the
+// workgroup reads whole K and V token rows (all G heads' 2D-byte slices) of
+// every page at one time. A sequence whose units lie in one range is
+// finished there; one that straddles ranges leaves one state per range
+// (ds_state), merged in range order by decode_stream_merge, so the result
+// does not depend on timing. A range's first sequence, when it began in an
+// earlier range, keeps its state in registers until the range's end: a
+// store in mid-stream would hold up the next tile's wait.
+// Per tile a wavefront moves K, V and its QPG query rows into an LDS stage
+// by direct buffer->LDS loads; the table entries of 64 tiles at a time come
+// the same way, a window ahead. Tile arithmetic is decode_tiles'.
+constexpr int DS_MAX_B = 1024;  // sequences per call on this path (LDS prefix table)
+
+// Integer division has no instruction; the 32-bit routine is a few times
+// shorter than the 64-bit one, and the products fit it at usual sizes.
+TSL_DEV int ds_div(uint64_t num, uint32_t den) {
+    return (int)((num >> 32) == 0 ? (uint32_t)num / den : num / den);
+}
+TSL_DEV int ds_start(int w, int U, int W) { return ds_div((uint64_t)w * U, W); }
+// The range holding unit u: the largest w with ds_start(w) <= u.
+TSL_DEV int ds_owner(int u, int U, int W) { return min(ds_div((uint64_t)(u + 1) * W - 1, U), W - 1); }
+// The range after w that holds units (every range does when U >= W); W
+// after the last range, so that a walk over ranges always ends.
+TSL_DEV int ds_next(int w, int U, int W) {
+    return w >= W - 1 ? W : U >= W ? w + 1 : ds_owner(ds_start(w + 1, U, W), U, W);
+}
+
+#define DS_WAIT_CASE(n) \
+    case n: asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory"); break;
+// Waits until at most n vector-memory loads of this wavefront are in flight.
+TSL_DEV void ds_wait(int n) {
+    switch (n) {
+        DS_WAIT_CASE(0) DS_WAIT_CASE(1) DS_WAIT_CASE(2) DS_WAIT_CASE(3) DS_WAIT_CASE(4) DS_WAIT_CASE(5)
+        DS_WAIT_CASE(6) DS_WAIT_CASE(7) DS_WAIT_CASE(8) DS_WAIT_CASE(9) DS_WAIT_CASE(10) DS_WAIT_CASE(11)
+        DS_WAIT_CASE(12) DS_WAIT_CASE(13) DS_WAIT_CASE(14) DS_WAIT_CASE(15) DS_WAIT_CASE(16) DS_WAIT_CASE(17)
+        DS_WAIT_CASE(18) DS_WAIT_CASE(19) DS_WAIT_CASE(20) DS_WAIT_CASE(21) DS_WAIT_CASE(22) DS_WAIT_CASE(23)
+        DS_WAIT_CASE(24) DS_WAIT_CASE(25) DS_WAIT_CASE(26) DS_WAIT_CASE(27) DS_WAIT_CASE(28) DS_WAIT_CASE(29)
+        DS_WAIT_CASE(30)
+        default: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
+    }
+}
+#undef DS_WAIT_CASE
+
+template <int D, int QPG>
+struct DsGeom {
+    static constexpr int ROWB = 2 * D, TILE = TT * ROWB, NLD = TILE / 1024;
+    static constexpr int QB = QPG * D * 2, NQ = (QB + 1023) / 1024;
+    static constexpr int WSTAGE = 2 * TILE + NQ * 1024;  // K, V, Q
+    static constexpr int LPT = 2 * NLD + NQ;             // loads per tile
+    static constexpr int ST = QPG * (4 + D);             // floats per state: [QPG][m, l, pad, pad, acc[D]]
+};
+// Range states: piece p < DS_PM of sequence b (its p-th range) at
+// [b][g][p] (so the merge reads them without first finding the ranges),
+// later pieces at [DS_PM B G + (w 2 + slot) G + g], slot 1 for a range's
+// last sequence when it is not also its first.
+constexpr int DS_PM = 8;
+TSL_DEV long ds_state(int b, int g, int p, int w, int slot, int B, int G) {
+    return p < DS_PM ? ((long)b * G + g) * DS_PM + p : (long)DS_PM * B * G + ((long)w * 2 + slot) * G + g;
+}
+// LDS bytes of a decode_stream workgroup: the rings, the table windows, the
+// unit prefix and lens.
+constexpr int ds_lds(int D, int QPG, int NWV, int STG) {
+    return NWV * STG * (2 * TT * 2 * D + (QPG * D * 2 + 1023) / 1024 * 1024) + NWV * 512 + (2 * DS_MAX_B + 1) * 4;
+}
+// LDS stages per wavefront: 3 (2 tiles in flight) where they fit, else 2
+// (0: the shape does not fit).
+constexpr int ds_stages(int D, int QPG, int NWV) {
+    return ds_lds(D, QPG, NWV, 3) <= 163840 ? 3 : ds_lds(D, QPG, NWV, 2) <= 163840 ? 2 : 0;
+}
+
+template <int D, int QPG, int NWV, int STG>
+__global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
+    using Gm = DsGeom<D, QPG>;
+    constexpr int ROWB = Gm::ROWB, KCH = D / 8, TILE = Gm::TILE, NLD = Gm::NLD, RPL = 1024 / ROWB;
+    constexpr int NQ = Gm::NQ, WSTAGE = Gm::WSTAGE, LPT = Gm::LPT;
+    constexpr float LAZY = 8.0f;
+    constexpr int LDS = ds_lds(D, QPG, NWV, STG);
+    static_assert(LDS == NWV * STG * WSTAGE + NWV * 512 + (2 * DS_MAX_B + 1) * 4 && LDS <= 163840, "LDS");
+    static_assert(2 * LPT + 2 <= 30, "ds_wait covers the loads in flight");
+    __shared__ __attribute__((aligned(16))) char lds[LDS];
+    int* wsl = reinterpret_cast<int*>(lds + NWV * STG * WSTAGE);  // [NWV][2][64] table windows
+    int* pre = wsl + NWV * 128;                                   // [B + 1] first unit of b
+    int* ln = pre + DS_MAX_B + 1;                                 // [B] lens
+
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, col = lane & 15;
+    const int g = __builtin_amdgcn_readfirstlane(tid >> 6);  // the wavefront's kv head
+    const int W = gridDim.x, w = blockIdx.x;
+    const int tpp = a.P / TT;
+
+    if (g == 0) {  // prefix of the units per sequence
+        int run = 0;
+        for (int b0 = 0; b0 < a.B; b0 += 64) {
+            const int b = b0 + lane;
+            const int n = b < a.B ? a.lens[b] : 0;
+            const int t = n > 0 ? ((n + a.P - 1) >> a.pshift) * tpp : 0;
+            int x = t;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(x, o);
+                if (lane >= o) x += y;
+            }
+            if (b < a.B) {
+                pre[b] = run + x - t;
+                ln[b] = n;
+            }
+            run += __shfl(x, 63);
+        }
+        if (lane == 0) pre[a.B] = run;
+    }
+    __syncthreads();
+    const int U = pre[a.B];
+    if (w == 0)
+        for (int x = tid; x <= a.B; x += 64 * NWV) a.pre[x] = pre[x];
+    for (int b = w; b < a.B; b += W)  // lens 0: 0 / 0, as the .tl computes
+        if (pre[b + 1] == pre[b])
+            for (int x = tid; x < a.H * D; x += 64 * NWV) a.O[(long)b * a.H * D + x] = f2h(0.0f / 0.0f);
+    const int u0 = ds_start(w, U, W), u1 = ds_start(w + 1, U, W), nt = u1 - u0;
+    if (nt <= 0) return;
+
+    // Window k: lane l describes unit u0 + 64 k + l (clamped to the range):
+    // its sequence, first token and length, and the flat table index of its page.
+    auto window = [&](int k, int& wb, int& wt, int& wn, int& widx) {
+        const int u = min(u0 + 64 * k + lane, u1 - 1);
+        int lo = 0, hi = a.B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (pre[mid] <= u) lo = mid;
+            else hi = mid - 1;
+        }
+        wb = lo;
+        wt = (u - pre[lo]) * TT;
+        wn = ln[lo];
+        const int pi = wt >> a.pshift;
+        widx = pi < a.MP ? lo * a.MP + pi : 0;  // tiles past the table read page 0
+    };
+
+    const long tok_bytes = (long)a.G * D * 2;
+    uint32_t offk[NLD], offv[NLD];
+#pragma unroll
+    for (int q = 0; q < NLD; q++) {
+        const int row = q * RPL + lane / KCH, pc = lane % KCH;
+        offk[q] = (uint32_t)(row * tok_bytes + ((pc ^ tswz_k<D>(row)) * 16));
+        offv[q] = (uint32_t)(row * tok_bytes + ((pc ^ tswz_v<D>(row)) * 16));
+    }
+    const uint32_t lbase = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
+    const uint32_t ring0 = lbase + g * STG * WSTAGE;
+    const uint32_t wsl0 = lbase + NWV * STG * WSTAGE + g * 512;
+    const char* Kg = reinterpret_cast<const char*>(a.Kc) + (long)g * D * 2;
+    const char* Vg = reinterpret_cast<const char*>(a.Vc) + (long)g * D * 2;
+    const i32x4 rtab = buf_rsrc(a.table, (uint32_t)((long)a.B * a.MP * 4));
+
+    int ib, it, in, ipg;       // the issuing side's window
+    int nb = 0, nx = 0, nn = 0;  // the next window's (its pages land in LDS)
+    {
+        int idx;
+        window(0, ib, it, in, idx);
+        ipg = a.table[idx];
+    }
+    asm volatile("" ::"v"(ipg));  // window 0 has arrived before the first asynchronous load
+
+    auto issue = [&](int j) {  // tile j of the range into stage j % STG
+        if ((j & 63) == 0) {
+            if (j > 0) {
+                ib = nb;
+                it = nx;
+                in = nn;
+                ipg = wsl[(g * 2 + ((j >> 6) & 1)) * 64 + lane];
+            }
+            if (j + 64 < nt) {  // the next window's table entries, one load
+                int idx;
+                window((j >> 6) + 1, nb, nx, nn, idx);
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(
+                                 wsl0 + (((j >> 6) + 1) & 1) * 256),
+                             "v"((uint32_t)idx * 4u), "s"(rtab)
+                             : "memory");
+            }
+        }
+        const int jl = j & 63;
+        const int b = __builtin_amdgcn_readlane(ib, jl), t0 = __builtin_amdgcn_readlane(it, jl);
+        const int page = __builtin_amdgcn_readlane(ipg, jl);
+        const bool ok = page >= 0 && page < a.NP;  // outside the pool: zeros
+        const long shift = ((long)(ok ? page : 0) * a.P + (t0 & (a.P - 1))) * tok_bytes;
+        const uint32_t range = ok ? (uint32_t)(TT * tok_bytes) : 0u;
+        const i32x4 rk = buf_rsrc(Kg + shift, range), rv = buf_rsrc(Vg + shift, range);
+        const i32x4 rq = buf_rsrc(a.Q + ((long)b * a.H + g * QPG) * D, (uint32_t)Gm::QB);
+        const uint32_t sk = ring0 + (j % STG) * WSTAGE, sv = sk + TILE, sq = sv + TILE;
+#pragma unroll
+        for (int q = 0; q < NLD; q++) {
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(sk + q * 1024),
+                         "v"(offk[q]), "s"(rk)
+                         : "memory");
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(sv + q * 1024),
+                         "v"(offv[q]), "s"(rv)
+                         : "memory");
+        }
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sq + q * 1024),
+                         "v"((uint32_t)(lane * 16 + q * 1024)), "s"(rq)
+                         : "memory");
+    };
+    // Loads issued with tile j: its own and, every 64 tiles, the next window's.
+    auto loads_with = [&](int j) { return LPT + (((j & 63) == 0 && j + 64 < nt) ? 1 : 0); };
+
+    uint32_t kaddr[D / 32], vaddr[D / 16];
+#pragma unroll
+    for (int s = 0; s < D / 32; s++) kaddr[s] = (uint32_t)(col * ROWB + (((4 * s + grp) ^ tswz_k<D>(col)) * 16));
+    const int vrow = 4 * grp + (col >> 2);
+#pragma unroll
+    for (int dt = 0; dt < D / 16; dt++) {
+        const int lc = 2 * dt + ((col & 3) >> 1);
+        vaddr[dt] = (uint32_t)(TILE + vrow * ROWB + ((lc ^ tswz_v<D>(vrow)) * 16) + 8 * (col & 1));
+    }
+    const uint32_t qaddr = (uint32_t)(2 * TILE + (col & (QPG - 1)) * D * 2 + grp * 16);
+
+    float m = -1e30f, lsum = 0.0f;
+    float4v acc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; dt++) acc[dt] = float4v{};
+
+    // Ends sequence b's part of this range: O directly when the whole
+    // sequence lies here, else this range's state for it.
+    // This range's state of sequence b (m, l, acc of its part), stored by
+    // the lanes that hold it.
+    auto store_state = [&](int b, float sm, float sl, const float4v* sa) {
+        const int lo = pre[b], wlo = ds_owner(lo, U, W);
+        int p = 0;  // which piece of b this range is
+        if (U >= W) p = w - wlo;
+        else
+            for (int x = wlo; x < w; x = ds_next(x, U, W)) p++;
+        const int slot = lo <= u0 ? 0 : 1;
+        float* pe = a.part + ds_state(b, g, p, w, slot, a.B, a.G) * Gm::ST + col * (4 + D);
+        if (col < QPG) {
+            if (grp == 0) *reinterpret_cast<float4v*>(pe) = float4v{sm, sl, 0.0f, 0.0f};
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++) *reinterpret_cast<float4v*>(pe + 4 + 16 * dt + 4 * grp) = sa[dt];
+        }
+    };
+    // Ends sequence b's part of this range before the range's end: O directly
+    // when the whole sequence lies here; else it is the range's first
+    // sequence, begun in an earlier range, and its state is held in
+    // registers until the end (a store now would stall the next tile's wait).
+    bool held = false;
+    float hm = 0.0f, hl = 0.0f;
+    float4v hacc[D / 16];
+    auto flush = [&](int b) {
+        float l = lsum + xor16(lsum);
+        l += xor32(l);
+        if (pre[b] >= u0) {
+            if (col < QPG) {
+                u16* o = a.O + ((long)b * a.H + g * QPG + col) * D + 4 * grp;
+#pragma unroll
+                for (int dt = 0; dt < D / 16; dt++) {
+                    half4 h;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) h[q] = (half_t)(acc[dt][q] / l);
+                    *reinterpret_cast<half4*>(o + 16 * dt) = h;
+                }
+            }
+        } else {
+            held = true;
+            hm = m;
+            hl = l;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++) hacc[dt] = acc[dt];
+        }
+    };
+
+    const int npre = min(nt, STG - 1);
+    for (int j = 0; j < npre; j++) issue(j);
+    int cwb = 0, cwt = 0, cwn = 0;  // the computing side's window
+    int cb = -1;                    // sequence being accumulated
+    for (int i = 0; i < nt; i++) {
+        const int ja = i + STG - 1;
+        if (ja < nt) issue(ja);
+        int after = 0;  // loads issued after tile i's
+        for (int j = i + 1; j <= min(ja, nt - 1); j++) after += loads_with(j);
+        ds_wait(after);
+        if ((i & 63) == 0) {
+            cwb = ib;
+            cwt = it;
+            cwn = in;
+        }
+        const int il = i & 63;
+        const int b = __builtin_amdgcn_readlane(cwb, il);
+        const int n = __builtin_amdgcn_readlane(cwn, il);
+        const int t0 = __builtin_amdgcn_readlane(cwt, il) + 4 * grp;  // token of register 0
+        if (b != cb) {
+            if (cb >= 0) flush(cb);
+            cb = b;
+            m = -1e30f;
+            lsum = 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++) acc[dt] = float4v{};
+        }
+        const char* sb = lds + (g * STG + i % STG) * WSTAGE;
+        float4v sc = float4v{};
+#pragma unroll
+        for (int s = 0; s < D / 32; s++) {
+            const half8 kop = *reinterpret_cast<const half8*>(sb + kaddr[s]);
+            half8 qop = *reinterpret_cast<const half8*>(sb + qaddr + s * 64);
+            if (col >= QPG) qop = half8{};
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop, sc, 0, 0, 0);
+        }
+        float x[4], mb = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            x[r] = t0 + r < n ? sc[r] * a.c2 : -INFINITY;
+            mb = fmaxf(mb, x[r]);
+        }
+        mb = fmaxf(mb, xor16(mb));
+        mb = fmaxf(mb, xor32(mb));
+        if (__builtin_amdgcn_ballot_w64(mb > m + LAZY) != 0) {
+            const float mn = fmaxf(m, mb);
+            const float alpha = __builtin_amdgcn_exp2f(m - mn);
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++) acc[dt] *= alpha;
+            m = mn;
+        }
+        half4 phi, plo;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float p = __builtin_amdgcn_exp2f(x[r] - m);
+            lsum += p;
+            phi[r] = (half_t)p;
+            plo[r] = (half_t)(p - (float)phi[r]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 16; dt++) {
+            const fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (__attribute__((address_space(3))) fp16x4_t*)(sb + vaddr[dt]));
+            const half4 vop = __builtin_bit_cast(half4, v);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, phi, acc[dt], 0, 0, 0);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vop, plo, acc[dt], 0, 0, 0);
+        }
+    }
+    // The last sequence: finished here when it began in this range and ends
+    // with it, else a state.
+    if (held) {  // the range's first sequence (it holds unit u0)
+        int bl = 0, bh = a.B - 1;
+        while (bl < bh) {
+            const int mid = (bl + bh + 1) >> 1;
+            if (pre[mid] <= u0) bl = mid;
+            else bh = mid - 1;
+        }
+        store_state(bl, hm, hl, hacc);
+    }
+    if (pre[cb] >= u0 && pre[cb + 1] <= u1) {
+        flush(cb);
+    } else {
+        float l = lsum + xor16(lsum);
+        l += xor32(l);
+        store_state(cb, m, l, acc);
+    }
+}
+
+// Merges the range states of each straddling (b, g), in range order (so the
+// bits do not depend on timing): one wavefront per (b, g). Lane e of a pass
+// owns 8 consecutive d of one query head. The first DS_PM pieces' states are
+// read together with the unit prefix (one memory round trip); more pieces
+// follow in batches of 8 ranges.
+template <int D, int QPG>
+__global__ __launch_bounds__(64) void decode_stream_merge(DecArgs a, int W) {
+    constexpr int ST = DsGeom<D, QPG>::ST, NE = QPG * D / 8;
+    const int b = blockIdx.x / a.G, g = blockIdx.x % a.G, lane = threadIdx.x;
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(a.part, 0, 0x7fffffff, 0x00020000);
+    for (int e0 = 0; e0 < NE; e0 += 64) {
+        const int e = min(e0 + lane, NE - 1), h = e / (D / 8), d0 = (e % (D / 8)) * 8;
+        auto load = [&](long st, float2v& ml, float4v& x0, float4v& x1) {
+            const uint32_t pe = (uint32_t)((st * ST + h * (4 + D)) * 4);
+            ml = __builtin_amdgcn_raw_buffer_load_b64(rp, pe, 0, 0);
+            x0 = __builtin_amdgcn_raw_buffer_load_b128(rp, pe + (4 + d0) * 4, 0, 0);
+            x1 = __builtin_amdgcn_raw_buffer_load_b128(rp, pe + (8 + d0) * 4, 0, 0);
+        };
+        float2v ml[DS_PM];
+        float4v x0[DS_PM], x1[DS_PM];
+#pragma unroll
+        for (int p = 0; p < DS_PM; p++) load(ds_state(b, g, p, 0, 0, a.B, a.G), ml[p], x0[p], x1[p]);
+        const int U = a.pre[a.B], lo = a.pre[b], hi = a.pre[b + 1];
+        if (hi <= lo) return;  // lens 0: written by decode_stream
+        const int wlo = ds_owner(lo, U, W), whi = ds_owner(hi - 1, U, W);
+        if (wlo == whi) return;  // finished by its range
+        int np = 1, wn = wlo;    // pieces, and the range after the first DS_PM
+        for (int x = wlo; x < whi; x = ds_next(x, U, W)) {
+            if (np == DS_PM) wn = x;
+            np++;
+        }
+        float M = -INFINITY, L = 0.0f, A[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) A[q] = 0.0f;
+        // Folds a batch of n states into (M, L, A): the batch maximum first.
+        auto fold = [&](int n) {
+            float Mb = M;
+#pragma unroll
+            for (int p = 0; p < DS_PM; p++)
+                if (p < n) Mb = fmaxf(Mb, ml[p][0]);
+            const float sc = __builtin_amdgcn_exp2f(M - Mb);
+            L *= sc;
+#pragma unroll
+            for (int q = 0; q < 8; q++) A[q] *= sc;
+#pragma unroll
+            for (int p = 0; p < DS_PM; p++) {
+                if (p < n) {
+                    const float f = __builtin_amdgcn_exp2f(ml[p][0] - Mb);
+                    L += ml[p][1] * f;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        A[q] += x0[p][q] * f;
+                        A[4 + q] += x1[p][q] * f;
+                    }
+                }
+            }
+            M = Mb;
+        };
+        fold(min(np, DS_PM));
+        if (np > DS_PM) {
+            // Every piece past the first is its range's first sequence: slot 0.
+            wn = ds_next(wn, U, W);  // the range of piece DS_PM
+            for (int p0 = DS_PM; p0 < np; p0 += DS_PM) {
+#pragma unroll
+                for (int p = 0; p < DS_PM; p++) {
+                    const int wq = min(wn, whi);
+                    load(ds_state(b, g, DS_PM, wq, 0, a.B, a.G), ml[p], x0[p], x1[p]);
+                    if (p0 + p + 1 < np) wn = ds_next(wn, U, W);
+                }
+                fold(min(np - p0, DS_PM));
+            }
+        }
+        if (e0 + lane < NE) {
+            half8 o;
+#pragma unroll
+            for (int q = 0; q < 8; q++) o[q] = (half_t)(A[q] / L);
+            *reinterpret_cast<half8*>(a.O + ((long)b * a.H + g * QPG + h) * D + d0) = o;
+        }
+    }
+}
+
+// Persistent workgroups of the stream path: one per CU.
+int stream_groups() { return num_cus(); }
+
+// Bytes of the stream path's range states: DS_PM per (b, g), then two per
+// (range, g) (ds_state).
+size_t stream_state_bytes(const TslKernel& k) {
+    const int64_t H = k.dim("H"), G = k.name == "paged_attention" ? H : k.dim("G");
+    const int64_t st = (H / G) * (4 + k.dim("D")) * 4;
+    return (size_t)((DS_PM * k.dim("B") * G + (int64_t)stream_groups() * 2 * G) * st);
+}
+
+template <int D, int QPG, int NWV>
+int run_decode_stream(DecArgs& a, hipStream_t s) {
+    constexpr int STG = ds_stages(D, QPG, NWV);
+    if constexpr (STG == 0) {
+        return tsl_fail(-2, "decode_attention: no stream variant");
+    } else {
+    const int W = stream_groups();
+    hipLaunchKernelGGL((decode_stream<D, QPG, NWV, STG>), dim3(W), dim3(64 * NWV), 0, s, a);
+    int r = TSL_LAUNCHED("decode_attention");
+    if (r) return r;
+    hipLaunchKernelGGL((decode_stream_merge<D, QPG>), dim3(a.B * a.G), dim3(64), 0, s, a, W);
+    return TSL_LAUNCHED("decode_attention merge");
+    }
+}
+
+template <int D>
+int run_stream_d(DecArgs& a, int qpg, hipStream_t s) {
+    if (a.G == 8) {
+        switch (qpg) {
+            case 2: return run_decode_stream<D, 2, 8>(a, s);
+            case 4: return run_decode_stream<D, 4, 8>(a, s);
+            case 8: return run_decode_stream<D, 8, 8>(a, s);
+        }
+    } else {
+        switch (qpg) {
+            case 2: return run_decode_stream<D, 2, 4>(a, s);
+            case 4: return run_decode_stream<D, 4, 4>(a, s);
+            case 8: return run_decode_stream<D, 8, 4>(a, s);
+        }
+    }
+    return tsl_fail(-2, "decode_attention: no stream variant");
+}
+
 template <int D, int QPG>
 int run_decode_tiles(DecArgs& a, hipStream_t s) {
     constexpr int WIDE = D == 64 ? 8 : 4;  // wavefronts per workgroup of a one-chunk table (rings fit LDS)
@@ -540,6 +1032,17 @@ int run_tiles_d(DecArgs& a, int qpg, hipStream_t s) {
 }
 
 bool tiles_path(int64_t D, int64_t P) { return (D == 64 || D == 128) && P % TT == 0; }
+
+// The balanced path: matrix-core shapes with 4 or 8 kv heads (a wavefront
+// each), 2-8 query heads per kv head, tables longer than one chunk, at most
+// DS_MAX_B sequences and 32-bit flat table offsets.
+bool stream_path(const TslKernel& k) {
+    const int64_t H = k.dim("H"), G = k.name == "paged_attention" ? H : k.dim("G");
+    const int64_t qpg = G > 0 ? H / G : 0;
+    return tiles_path(k.dim("D"), k.dim("P")) && (G == 4 || G == 8) && (qpg == 2 || qpg == 4 || qpg == 8) &&
+           ds_stages((int)k.dim("D"), (int)qpg, (int)G) > 0 &&
+           k.dim("MP") > DEC_WIDE_MAX_PAGES && k.dim("B") <= DS_MAX_B && k.dim("B") * k.dim("MP") * 4 < (1LL << 32);
+}
 
 template <int D, int QPG>
 int run_decode(DecArgs& a, hipStream_t s) {
@@ -593,6 +1096,12 @@ int prepare_decode(TslKernel& k) {
     int64_t qpg = H / G;
     if (qpg != 1 && qpg != 2 && qpg != 4 && qpg != 8 && qpg != 16)
         return tsl_fail(-2, k.name + ": H / G must be 1, 2, 4, 8 or 16");
+    if (stream_path(k)) {  // range states, then the [B + 1] unit prefix
+        size_t bytes = stream_state_bytes(k) + (size_t)(k.dim("B") + 1) * 4;
+        if (tsl_hip_check(hipMalloc(&k.scratch, bytes), "decode_attention scratch")) return -1;
+        k.scratch_bytes = bytes;
+        return 0;
+    }
     int nch = nchunks(k);
     if (nch > 1) {  // [B][G][NCH][QPG][2 + D] per-chunk states
         size_t bytes = (size_t)k.dim("B") * G * nch * qpg * (2 + D) * sizeof(float);
@@ -623,6 +1132,10 @@ static int launch_decode_common(TslKernel& k, const uint64_t* args, hipStream_t 
     a.part = reinterpret_cast<float*>(k.scratch);
     if (a.B == 0) return 0;
     const int D = k.dim("D"), qpg = a.H / a.G;
+    if (stream_path(k)) {
+        a.pre = reinterpret_cast<int*>(reinterpret_cast<char*>(k.scratch) + stream_state_bytes(k));
+        return D == 128 ? run_stream_d<128>(a, qpg, s) : run_stream_d<64>(a, qpg, s);
+    }
     if (tiles_path(D, a.P)) return D == 128 ? run_tiles_d<128>(a, qpg, s) : run_tiles_d<64>(a, qpg, s);
     switch (D) {
         case 16: return run_decode_d<16>(a, qpg, s);

@@ -276,7 +276,14 @@ def _decode(q, kc, vc, table, lens, scale):
                                  dict(b=5, h=4, g=2, d=16, p=8, lo=0, hi=60),
                                  dict(b=3, h=8, g=8, d=32, p=16, lo=1, hi=300),
                                  dict(b=6, h=16, g=1, d=128, p=64, lo=1, hi=3000),
-                                 dict(b=9, h=8, g=4, d=64, p=32, lo=0, hi=2100)])
+                                 dict(b=9, h=8, g=4, d=64, p=32, lo=0, hi=2100),
+                                 # tables longer than 64 pages take the balanced (persistent) path:
+                                 # fewer units than workgroups, many short sequences (lens 0
+                                 # among them) under a long table, P 64, 3-stage rings
+                                 dict(b=1, h=32, g=8, d=128, p=16, lo=1100, hi=1100),
+                                 dict(b=40, h=32, g=8, d=64, p=16, lo=0, hi=40, mp=80),
+                                 dict(b=3, h=16, g=4, d=128, p=64, lo=1, hi=9000),
+                                 dict(b=17, h=32, g=4, d=128, p=16, lo=2000, hi=5000)])
 def test_decode_attention_vs_oracle(cfg):
     _say("decode", cfg)
     q, kc, vc, table, lens, scale = decode_case(1, **cfg)
