@@ -94,10 +94,20 @@ TSL_DEV void rms_store(const float (&v)[NV][E], float rs, const u16* __restrict_
         const int c = (i * 64 + lane) * E;
         if (vec && c + E <= ncols) {
             // E outputs: 8 halves (16 bytes) for f16 input rows, 4 (8 bytes) for f32.
+            // The weights' E halves in one load (the row's chunk is aligned alike).
+            uint32_t wv[E / 2];
+            if constexpr (E == 8) {
+                const u32x4 t = *reinterpret_cast<const u32x4*>(W + c);
+                for (int p = 0; p < 4; p++) wv[p] = t[p];
+            } else {
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 t = *reinterpret_cast<const u32x2*>(W + c);
+                for (int p = 0; p < 2; p++) wv[p] = t[p];
+            }
             uint32_t o[E / 2];
             for (int p = 0; p < E / 2; p++) {
-                u16 lo = f2h(v[i][2 * p] * rs * h2f(W[c + 2 * p]));
-                u16 hi = f2h(v[i][2 * p + 1] * rs * h2f(W[c + 2 * p + 1]));
+                u16 lo = f2h(v[i][2 * p] * rs * h2f((u16)(wv[p] & 0xffff)));
+                u16 hi = f2h(v[i][2 * p + 1] * rs * h2f((u16)(wv[p] >> 16)));
                 o[p] = (uint32_t)lo | ((uint32_t)hi << 16);
             }
             if constexpr (E == 8) {
