@@ -12,8 +12,11 @@ events on the library's stream, bracketed by stream synchronisation.
                 restatement) on a bounded sample of the same GEMM's programs;
   cases         the other BASELINE configs measured the same way: GEMM
                 1024^3/2048^3, causal FlashAttention H32 D64 S 512..4096,
-                paged GQA decode (GB/s against 8 TB/s), RMSNorm and softmax
-                4096^2, and TinyLlama-shape decode tokens/s (skip with --no-llm).
+                paged GQA decode (GB/s against 8 TB/s), paged_attention (G = H),
+                the engine's prefill_attention and its five projections at
+                decode (32 rows, GB/s) and prefill (1024 rows, TFLOP/s) sizes,
+                RMSNorm and softmax 4096^2, and TinyLlama-shape decode tokens/s
+                (skip with --no-llm).
 """
 
 import argparse
@@ -174,6 +177,75 @@ def rows_case(T, kind):
     return Timed(T, k, bufs), 4.0 * r * c
 
 
+def prefill_case(T, seed=4, lens=(512, 512), h=32, g=4, d=64):
+    """kernels/llm.tl prefill_attention at the engine's prefill step
+    (two 512-token prompts packed into 1024 rows)."""
+    rng = np.random.default_rng(seed)
+    t = sum(lens)
+    q = f16(rng.standard_normal((t, h, d), np.float32))
+    k, v = (f16(rng.standard_normal((t, g, d), np.float32)) for _ in range(2))
+    starts = np.concatenate([np.full(l, sum(lens[:i]), np.int32) for i, l in enumerate(lens)])
+    bufs = [T.tensor(q), T.tensor(k), T.tensor(v), T.tensor(starts), T.alloc(q.nbytes), T.F32(1.0 / np.sqrt(d))]
+    kern = T.kernel("llm", "prefill_attention", [q.shape, k.shape, v.shape, starts.shape, q.shape])
+    flops = sum(2.0 * h * l * l * d for l in lens)  # the causal half of 4 H L^2 D per prompt
+    return Timed(T, kern, bufs), flops
+
+
+# The TinyLlama projections (BASELINE config 5: dim 2048, QKV 2560, FFN 5632,
+# vocab 32000) as the engine runs them: name, K, N.
+PROJ = (("linear", 2048, 2560, "qkv"), ("linear_residual", 2048, 2048, "o"), ("gate_up", 2048, 5632, "gate_up"),
+        ("linear_residual", 5632, 2048, "down"), ("logits", 2048, 32000, "logits"))
+
+
+def proj_case(T, name, m, k, n, seed=6):
+    """One kernels/llm.tl projection X[m, k] W^T. Returns the timer, its
+    flops and the HBM bytes it must move (weights once, X, Y, and R read and
+    written for linear_residual)."""
+    rng = np.random.default_rng(seed)
+    x = f16(rng.standard_normal((m, k), np.float32))
+    ws = [f16(rng.standard_normal((n, k), np.float32) / np.float32(np.sqrt(k)))
+          for _ in range(2 if name == "gate_up" else 1)]
+    if name == "linear_residual":
+        y = T.tensor(np.zeros((m, n), np.float32))
+        ybytes = 8 * m * n
+    elif name == "logits":
+        y = T.alloc(4 * m * n)
+        ybytes = 4 * m * n
+    else:
+        y = T.alloc(2 * m * n)
+        ybytes = 2 * m * n
+    bufs = [T.tensor(x)] + [T.tensor(w) for w in ws] + [y]
+    kern = T.kernel("llm", name, [x.shape] + [w.shape for w in ws] + [(m, n)])
+    flops = 2.0 * m * n * k * len(ws)
+    nbytes = 2.0 * n * k * len(ws) + 2.0 * m * k + ybytes
+    return Timed(T, kern, bufs), flops, nbytes
+
+
+def paged_case(T, seed=3, b=16, h=32, d=128, p=16):
+    """kernels/attention.tl paged_attention (G = H) with context lengths
+    ~ U[128, 4096] and pages by seeded permutation, as decode_case."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(128, 4097, b).astype(np.int32)
+    need = (lens + p - 1) // p
+    mp = 256
+    npages = int(need.sum())
+    perm = rng.permutation(npages).astype(np.int32)
+    table = np.zeros((b, mp), np.int32)
+    o = 0
+    for i in range(b):
+        table[i, :need[i]] = perm[o:o + need[i]]
+        o += need[i]
+    q = f16(rng.standard_normal((b, h, d), np.float32))
+    kc = f16(rng.standard_normal((npages, p, h, d), np.float32))
+    vc = f16(rng.standard_normal((npages, p, h, d), np.float32))
+    bufs = [T.tensor(q), T.tensor(kc), T.tensor(vc), T.tensor(table), T.tensor(lens), T.alloc(b * h * d * 2),
+            T.F32(1.0 / np.sqrt(d))]
+    kern = T.kernel("attention", "paged_attention", [[b, h, d], [npages, p, h, d], [npages, p, h, d], [b, mp], [b],
+                                                     [b, h, d]])
+    nbytes = float(lens.sum()) * h * d * 2 * 2 + b * h * d * 2 * 2 + 4 * b * mp + 4 * b
+    return Timed(T, kern, bufs), nbytes
+
+
 def llm_case(T, seqs=32, prompt=512, new=128, graphs=True):
     """TinyLlama-1.1B shape, random fp16 weights, 32
     prompts of 512 random ids, 128 greedy steps under continuous batching."""
@@ -211,7 +283,8 @@ def main():
     ap.add_argument("--no-llm", action="store_true", help="skip the TinyLlama decode case")
     ap.add_argument("--no-graphs", action="store_true",
                     help="TinyLlama case: launch decode steps kernel by kernel (for kernel traces)")
-    ap.add_argument("--only", default="", help="comma list of cases: gemm1024,gemm2048,fa512..fa4096,decode,"
+    ap.add_argument("--only", default="", help="comma list of cases: gemm1024,gemm2048,fa512..fa4096,decode,paged,"
+                    "prefill,proj,"
                     "rmsnorm,softmax,llm,copy (counter calibration); 'none' for the headline GEMM alone")
     ap.add_argument("--profile", action="store_true",
                     help="few launches, no clock warm-up: for rocprofv3 counter passes")
@@ -287,6 +360,32 @@ def main():
                           "gbps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4), "bytes": nb,
                           "context_tokens": toks, "tflops": round(fl / m / 1e9, 3),
                           "traffic": load_traffic("decode_attention")})
+        if want("paged"):
+            t, nb = paged_case(T)
+            t.warm()
+            m = t.median(50)
+            cases.append({"case": "paged_attention B16 H32 D128 P16 ctx~U[128,4096]", "ms": round(m, 5),
+                          "gbps": round(nb / m / 1e6, 1), "frac_hbm": round(nb / m / 1e6 / PEAK_HBM, 4)})
+        if want("prefill"):
+            t, fl = prefill_case(T)
+            t.warm()
+            m = t.median(50)
+            cases.append({"case": "prefill_attention T1024 (2 x 512 packed) H32 G4 D64", "ms": round(m, 5),
+                          "tflops": round(fl / m / 1e9, 2), "frac_mfma": round(fl / m / 1e9 / PEAK_MFMA_F16, 4)})
+        if want("proj"):
+            # Decode-sized (32 rows: a weight stream, HBM-bound) and
+            # prefill-sized (1024 rows: MFMA-bound) engine projections.
+            for name, k, n, label in PROJ:
+                for rows in (32, 1024):
+                    t, fl, nb = proj_case(T, name, rows, k, n)
+                    t.warm()
+                    m = t.median(50)
+                    c = {"case": f"{label} ({name}) M{rows} N{n} K{k}", "ms": round(m, 5)}
+                    if rows == 32:
+                        c.update(gbps=round(nb / m / 1e6, 1), frac_hbm=round(nb / m / 1e6 / PEAK_HBM, 4))
+                    else:
+                        c.update(tflops=round(fl / m / 1e9, 2), frac_mfma=round(fl / m / 1e9 / PEAK_MFMA_F16, 4))
+                    cases.append(c)
         if "copy" in only:  # counter calibration (rocprofv3 passes), not a bench line
             n = 32 << 20
             bufs = [T.alloc(4 * n), T.alloc(4 * n), T.alloc(4 * n)]
