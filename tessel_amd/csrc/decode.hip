@@ -650,7 +650,7 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
         wt = (u - pre[lo]) * TT;
         wn = ln[lo];
         const int pi = wt >> a.pshift;
-        widx = pi < a.MP ? lo * a.MP + pi : 0;  // tiles past the table read page 0
+        widx = pi < a.MP ? lo * a.MP + pi : 0;  // (past the table: any in-range entry; issue reads page 0)
     };
 
     const long tok_bytes = (long)a.G * D * 2;
@@ -696,7 +696,8 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
         }
         const int jl = j & 63;
         const int b = __builtin_amdgcn_readlane(ib, jl), t0 = __builtin_amdgcn_readlane(it, jl);
-        const int page = __builtin_amdgcn_readlane(ipg, jl);
+        // Tiles past the table read pool page 0 (their window entry is a stand-in).
+        const int page = (t0 >> a.pshift) < a.MP ? __builtin_amdgcn_readlane(ipg, jl) : 0;
         const bool ok = page >= 0 && page < a.NP;  // outside the pool: zeros
         const long shift = ((long)(ok ? page : 0) * a.P + (t0 & (a.P - 1))) * tok_bytes;
         const uint32_t range = ok ? (uint32_t)(TT * tok_bytes) : 0u;

@@ -313,9 +313,12 @@ def test_decode_attention_repeat_launches():
         T.free(x)
 
 
-def test_decode_attention_indexing_properties():
-    _say("decode properties")
-    q, kc, vc, table, lens, scale = decode_case(2, b=16, h=32, g=8, d=128, p=16, lo=1, hi=1000)
+@pytest.mark.parametrize("mp", [None, 100])
+def test_decode_attention_indexing_properties(mp):
+    # mp None: tables of at most 64 pages (the single-chunk form); 100: the
+    # balanced form, whose range boundaries move with every sequence's length.
+    _say("decode properties", mp)
+    q, kc, vc, table, lens, scale = decode_case(2, b=16, h=32, g=8, d=128, p=16, lo=1, hi=1000, mp=mp)
     base = _decode(q, kc, vc, table, lens, scale)
     # The same tokens at other pool positions: bit-identical (only the token order matters).
     perm = np.random.default_rng(3).permutation(kc.shape[0])
@@ -328,16 +331,21 @@ def test_decode_attention_indexing_properties():
     t2[5, 1] = -7
     want = oracle.decode_attention(q, kc, vc, t2, lens, scale, threads=8)
     parity("decode oob pages", _decode(q, kc, vc, t2, lens, scale), want)
-    # lens 0 gives NaN rows; the rest unchanged.
+    # lens 0 gives NaN rows; the rest unchanged (bit for bit where the work
+    # split does not depend on the lengths, else within the tolerance).
     l0 = lens.copy()
     l0[[2, 9]] = 0
     got = _decode(q, kc, vc, table, l0, scale)
     assert np.isnan(got[[2, 9]].astype(np.float32)).all()
     keep = [i for i in range(16) if i not in (2, 9)]
-    np.testing.assert_array_equal(got[keep].view(np.uint16), base[keep].view(np.uint16))
+    if mp is None:
+        np.testing.assert_array_equal(got[keep].view(np.uint16), base[keep].view(np.uint16))
+    else:
+        parity("decode lens 0 rest", got[keep], base[keep])
     # Tokens past the table's MP * P read page 0 (the interpreter's out-of-range load).
-    tb = np.ascontiguousarray(table[:, :8])
-    l3 = np.minimum(lens, 8 * 16 + 40).astype(np.int32)
+    w = 8 if mp is None else 70
+    tb = np.ascontiguousarray(table[:, :w])
+    l3 = np.minimum(lens + (0 if mp is None else 200), w * 16 + 40).astype(np.int32)
     want = oracle.decode_attention(q, kc, vc, tb, l3, scale, threads=8)
     parity("decode past table", _decode(q, kc, vc, tb, l3, scale), want)
 
