@@ -342,6 +342,17 @@ def test_decode_attention_indexing_properties(mp):
         np.testing.assert_array_equal(got[keep].view(np.uint16), base[keep].view(np.uint16))
     else:
         parity("decode lens 0 rest", got[keep], base[keep])
+    # NaN garbage past lens inside a sequence's last page: the .tl loads whole
+    # pages, so V's reaches the output (p = 0 times NaN), while K's is masked
+    # off before it counts.
+    ragged = np.flatnonzero(lens % 16 != 0)
+    bv, bk = int(ragged[0]), int(ragged[1])
+    kn, vn = kc.copy(), vc.copy()
+    vn[table[bv, (lens[bv] - 1) // 16], lens[bv] % 16] = np.nan
+    kn[table[bk, (lens[bk] - 1) // 16], lens[bk] % 16] = np.nan
+    want = oracle.decode_attention(q, kn, vn, table, lens, scale, threads=8)
+    assert np.isnan(want[bv].astype(np.float32)).any() and not np.isnan(want[bk].astype(np.float32)).any()
+    parity("decode nan past lens", _decode(q, kn, vn, table, lens, scale), want)
     # Tokens past the table's MP * P read page 0 (the interpreter's out-of-range load).
     w = 8 if mp is None else 70
     tb = np.ascontiguousarray(table[:, :w])
