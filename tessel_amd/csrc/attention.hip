@@ -68,7 +68,12 @@ TSL_DEV int swz_v(int key) {  // in 16-byte chunks
     else return 0;
 }
 
-template <int D, bool PREFILL>
+// KS = 2 (short sequences): the 4 wavefronts form 2 query groups of 32 rows,
+// and the 2 wavefronts of a group take alternate key blocks (block b to
+// wavefront b % 2, each block with its own LDS stages), so a workgroup's
+// critical path is half its keys; the two states of each row are merged
+// through LDS at the end (max, then the rescaled sums, in wavefront order).
+template <int D, bool PREFILL, int KS>
 __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     constexpr int DP = D < 32 ? 32 : D;     // V^T rows, padded to one MFMA tile
     constexpr int KCH = D / 8;              // 16-byte chunks per row
@@ -78,11 +83,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     constexpr int LPW = NL >= 4 ? NL / 4 : 1;  // loads per wave per matrix (waves >= NL idle when NL < 4)
     constexpr int STAGE = 2 * BKEY * ROWB;  // K then V
     constexpr float LAZY = 8.0f;            // rescale only when the max grows by more than 2^8
-    __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+    constexpr int BQW = BQ / KS;            // queries per workgroup
+    static_assert(KS == 1 || KS == 2, "key split");
+    constexpr int NF = 2 + 16 * (DP / 32);  // floats per lane of a merged state: mc, lsum, acc
+    constexpr int LDSB = KS * 2 * STAGE > 4 * NF * 64 * 4 || KS == 1 ? KS * 2 * STAGE : 4 * NF * 64 * 4;
+    __shared__ __attribute__((aligned(16))) char lds[LDSB];  // [ks][stage]; at the end, the merge
 
     const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nqb = (a.S + BQ - 1) / BQ;
+    const int qg = wave / KS, ks = wave % KS;  // query group, key split
+    const int nqb = (a.S + BQW - 1) / BQW;
     // Work rank (0 = most keys): longest first, and within every full round of
     // NCU workgroups (one per CU) alternately reversed, so the workgroups
     // sharing a CU (ranks j, 2 NCU-1-j, 2 NCU+j, ...) add up to the same work.
@@ -94,7 +104,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     const int qb = nqb - 1 - rank / a.H;
     const int h = rank % a.H;
     const int hk = PREFILL ? h / (a.H / a.G) : h;
-    const int q0 = qb * BQ, qw = q0 + wave * 32;
+    const int q0 = qb * BQW, qw = q0 + qg * 32;
     const int myq = qw + (lane & 31);
 
     const u16* Qh = a.Q + (long)h * a.q_head;
@@ -125,18 +135,26 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
         offk[i] = (uint32_t)(key * a.k_row * 2 + ((p ^ swz_k<D>(key)) * 16));
         offv[i] = (uint32_t)(key * a.k_row * 2 + ((p ^ swz_v<D>(key)) * 16));
     }
-    auto issue = [&](int j, int stage) {
-        const long shift = (long)j * a.k_row * 2;
-        const uint32_t range = (uint32_t)(((long)a.S - j) * a.k_row * 2);
-        const i32x4 rk = make_rsrc(Kh + shift, range), rv = make_rsrc(Vh + shift, range);
-        const uint32_t sk = lds_base + stage * STAGE + wave * LPW * 1024, sv = sk + BKEY * ROWB;
+    // Iteration it's key blocks it KS .. it KS + KS - 1 (those below nblk)
+    // into [ks][stage]; every wavefront loads its share of each.
+    auto issue = [&](int it, int stage, int kbeg, int nblk) {
 #pragma unroll
-        for (int i = 0; i < LPW; i++) {
-            if (!ldk[i]) continue;  // wave-uniform
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sk + i * 1024),
-                         "v"(offk[i]), "s"(rk));
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sv + i * 1024),
-                         "v"(offv[i]), "s"(rv));
+        for (int kk = 0; kk < KS; kk++) {
+            const int bi = it * KS + kk;
+            if (bi >= nblk) break;
+            const int j = kbeg + bi * BKEY;
+            const long shift = (long)j * a.k_row * 2;
+            const uint32_t range = (uint32_t)(((long)a.S - j) * a.k_row * 2);
+            const i32x4 rk = make_rsrc(Kh + shift, range), rv = make_rsrc(Vh + shift, range);
+            const uint32_t sk = lds_base + (kk * 2 + stage) * STAGE + wave * LPW * 1024, sv = sk + BKEY * ROWB;
+#pragma unroll
+            for (int i = 0; i < LPW; i++) {
+                if (!ldk[i]) continue;  // wave-uniform
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sk + i * 1024),
+                             "v"(offk[i]), "s"(rk));
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(sv + i * 1024),
+                             "v"(offv[i]), "s"(rv));
+            }
         }
     };
 
@@ -172,17 +190,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     for (int i = 0; i < DP / 32; i++) acc[i] = float16v{};
     const half2v ones = {(half_t)1.0f, (half_t)1.0f};
 
-    const int kend = min(q0 + BQ, a.S);
+    const int kend = min(q0 + BQW, a.S);
     const int kbeg = PREFILL ? (a.starts[q0] / BKEY) * BKEY : 0;
     const int nblk = kbeg < kend ? (kend - kbeg + BKEY - 1) / BKEY : 0;
-    if (nblk > 0) issue(kbeg, 0);
-    for (int b = 0; b < nblk; b++) {
-        const int j = kbeg + b * BKEY;
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of block b are in LDS
-        __syncthreads();                     // everyone's; and block b-1's reads of the other stage are done
-        if (b + 1 < nblk) issue(j + BKEY, (b + 1) & 1);
-        const char* st_base = lds + (b & 1) * STAGE;
-        const bool active = j <= qw + 31 && qw < a.S;  // some key of this block <= some query of the wave
+    const int nit = (nblk + KS - 1) / KS;
+    if (nit > 0) issue(0, 0, kbeg, nblk);
+    for (int it = 0; it < nit; it++) {
+        const int b = it * KS + ks, j = kbeg + b * BKEY;  // this wavefront's block
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of the iteration are in LDS
+        __syncthreads();                     // everyone's; and the last iteration's reads of the other stage are done
+        if (it + 1 < nit) issue(it + 1, (it + 1) & 1, kbeg, nblk);
+        const char* st_base = lds + (ks * 2 + (it & 1)) * STAGE;
+        const bool active = b < nblk && j <= qw + 31 && qw < a.S;  // some key of this block <= some query of the wave
         if (!active) continue;
         // S^T = K Q^T for the 64 keys x this wave's 32 queries (two 32-key tiles).
         float16v st[2];
@@ -260,6 +279,43 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
         }
     }
 
+    if constexpr (KS > 1) {
+        // Merge the KS states of each query group through LDS (the stages are
+        // idle): the max of the scaled running maxima, then the sums rescaled
+        // to it, in wavefront order. Lane layouts agree, so lane by lane.
+        float* st = reinterpret_cast<float*>(lds);  // [4 waves][NF][64]
+        static_assert(4 * NF * 64 * 4 <= LDSB, "merge area");
+        __syncthreads();
+        {
+            float* me = st + wave * NF * 64 + lane;
+            me[0] = mc;
+            me[64] = lsum;
+#pragma unroll
+            for (int dt = 0; dt < DP / 32; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) me[(2 + 16 * dt + r) * 64] = acc[dt][r];
+        }
+        __syncthreads();
+        if (ks != 0) return;
+        float M = mc;
+#pragma unroll
+        for (int k = 1; k < KS; k++) M = fmaxf(M, st[(wave + k) * NF * 64 + lane]);
+        if (M == -INFINITY) M = 0.0f;  // no key anywhere (rows past S): every factor below is 0
+        float L = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < DP / 32; dt++) acc[dt] = float16v{};
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            const float* o = st + (wave + k) * NF * 64 + lane;
+            const float f = __builtin_amdgcn_exp2f(o[0] - M);
+            L += o[64] * f;
+#pragma unroll
+            for (int dt = 0; dt < DP / 32; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[dt][r] += o[(2 + 16 * dt + r) * 64] * f;
+        }
+        lsum = L;
+    }
     const float l = lsum + xor32(lsum);
     if (myq < a.S) {
         u16* o = a.O + (long)myq * a.q_row + (long)h * a.q_head;
@@ -278,20 +334,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
 }
 
 
-template <bool PREFILL>
-int run_attn(AttnArgs a, int D, hipStream_t s, const char* what) {
-    if (a.S == 0 || a.H == 0) return 0;
-    a.ncu = num_cus();
-    dim3 grid(((a.S + BQ - 1) / BQ) * a.H);
+template <bool PREFILL, int KS>
+int run_attn_ks(AttnArgs a, int D, hipStream_t s, const char* what) {
+    dim3 grid(((a.S + BQ / KS - 1) / (BQ / KS)) * a.H);
     switch (D) {
-        case 16: hipLaunchKernelGGL((attn_fwd<16, PREFILL>), grid, dim3(256), 0, s, a); break;
-        case 32: hipLaunchKernelGGL((attn_fwd<32, PREFILL>), grid, dim3(256), 0, s, a); break;
-        case 64: hipLaunchKernelGGL((attn_fwd<64, PREFILL>), grid, dim3(256), 0, s, a); break;
-        case 128: hipLaunchKernelGGL((attn_fwd<128, PREFILL>), grid, dim3(256), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((attn_fwd<16, PREFILL, KS>), grid, dim3(256), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((attn_fwd<32, PREFILL, KS>), grid, dim3(256), 0, s, a); break;
+        case 64: hipLaunchKernelGGL((attn_fwd<64, PREFILL, KS>), grid, dim3(256), 0, s, a); break;
+        case 128: hipLaunchKernelGGL((attn_fwd<128, PREFILL, KS>), grid, dim3(256), 0, s, a); break;
         default: return tsl_fail(-2, std::string(what) + ": head dimension " + std::to_string(D) +
                                          " unsupported (16, 32, 64 or 128)");
     }
     return TSL_LAUNCHED(what);
+}
+
+template <bool PREFILL>
+int run_attn(AttnArgs a, int D, hipStream_t s, const char* what) {
+    if (a.S == 0 || a.H == 0) return 0;
+    a.ncu = num_cus();
+    // Key split 2 when 128-query workgroups would not give every CU a second
+    // one (H32 D64: S <= 1024 139 / 335 against 108 / 266 TFLOP/s at S 512 /
+    // 1024; the packed 2 x 512 prefill 201 against 165). Beyond that the
+    // split's halved K/V reuse costs more than the shorter critical path
+    // gains (S=4096: 659 against 779), and a split of 4 (its stages fill the
+    // LDS, one workgroup per CU) loses everywhere.
+    if ((long)((a.S + BQ - 1) / BQ) * a.H <= a.ncu) return run_attn_ks<PREFILL, 2>(a, D, s, what);
+    return run_attn_ks<PREFILL, 1>(a, D, s, what);
 }
 
 }  // namespace
