@@ -32,7 +32,8 @@ struct DecArgs {
     const int *table, *lens;
     u16* O;
     float* part;  // [B][G][NCH][QPG][2 + D]: m, l, acc (stream path: range states, see DsGeom)
-    int* pre;     // stream path: first unit of each sequence, [B + 1]
+    int* pre;     // stream path: first unit of each (virtual) sequence, [B NG + 1]
+    int NG;       // stream path: head groups of NWV kv heads per sequence
     int B, H, G, NP, P, MP, NCH;
     int CH;  // pages per chunk
     int pshift;  // log2(P) (P is a power of two)
@@ -606,11 +607,15 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
     const int W = gridDim.x, w = blockIdx.x;
     const int tpp = a.P / TT;
 
-    if (g == 0) {  // prefix of the units per sequence
+    // Virtual sequences vb = b NG + hg: sequence b's kv heads hg NWV ..
+    // hg NWV + NWV - 1 (NG = G / NWV head groups; 1 when the wavefronts
+    // cover all G heads), each its own run of units.
+    const int NG = a.NG, VB = a.B * NG;
+    if (g == 0) {  // prefix of the units per virtual sequence
         int run = 0;
-        for (int b0 = 0; b0 < a.B; b0 += 64) {
+        for (int b0 = 0; b0 < VB; b0 += 64) {
             const int b = b0 + lane;
-            const int n = b < a.B ? a.lens[b] : 0;
+            const int n = b < VB ? a.lens[b / NG] : 0;
             const int t = n > 0 ? ((n + a.P - 1) >> a.pshift) * tpp : 0;
             int x = t;
 #pragma unroll
@@ -618,21 +623,22 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
                 const int y = __shfl_up(x, o);
                 if (lane >= o) x += y;
             }
-            if (b < a.B) {
+            if (b < VB) {
                 pre[b] = run + x - t;
                 ln[b] = n;
             }
             run += __shfl(x, 63);
         }
-        if (lane == 0) pre[a.B] = run;
+        if (lane == 0) pre[VB] = run;
     }
     __syncthreads();
-    const int U = pre[a.B];
+    const int U = pre[VB];
     if (w == 0)
-        for (int x = tid; x <= a.B; x += 64 * NWV) a.pre[x] = pre[x];
-    for (int b = w; b < a.B; b += W)  // lens 0: 0 / 0, as the .tl computes
-        if (pre[b + 1] == pre[b])
-            for (int x = tid; x < a.H * D; x += 64 * NWV) a.O[(long)b * a.H * D + x] = f2h(0.0f / 0.0f);
+        for (int x = tid; x <= VB; x += 64 * NWV) a.pre[x] = pre[x];
+    for (int vb = w; vb < VB; vb += W)  // lens 0: 0 / 0, as the .tl computes (the group's heads)
+        if (pre[vb + 1] == pre[vb])
+            for (int x = tid; x < NWV * QPG * D; x += 64 * NWV)
+                a.O[((long)(vb / NG) * a.H + (vb % NG) * NWV * QPG) * D + x] = f2h(0.0f / 0.0f);
     const int u0 = ds_start(w, U, W), u1 = ds_start(w + 1, U, W), nt = u1 - u0;
     if (nt <= 0) return;
 
@@ -640,7 +646,7 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
     // its sequence, first token and length, and the flat table index of its page.
     auto window = [&](int k, int& wb, int& wt, int& wn, int& widx) {
         const int u = min(u0 + 64 * k + lane, u1 - 1);
-        int lo = 0, hi = a.B - 1;
+        int lo = 0, hi = VB - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
             if (pre[mid] <= u) lo = mid;
@@ -650,7 +656,7 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
         wt = (u - pre[lo]) * TT;
         wn = ln[lo];
         const int pi = wt >> a.pshift;
-        widx = pi < a.MP ? lo * a.MP + pi : 0;  // (past the table: any in-range entry; issue reads page 0)
+        widx = pi < a.MP ? (lo / NG) * a.MP + pi : 0;  // (past the table: any in-range entry; issue reads page 0)
     };
 
     const long tok_bytes = (long)a.G * D * 2;
@@ -664,8 +670,6 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
     const uint32_t lbase = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
     const uint32_t ring0 = lbase + g * STG * WSTAGE;
     const uint32_t wsl0 = lbase + NWV * STG * WSTAGE + g * 512;
-    const char* Kg = reinterpret_cast<const char*>(a.Kc) + (long)g * D * 2;
-    const char* Vg = reinterpret_cast<const char*>(a.Vc) + (long)g * D * 2;
     const i32x4 rtab = buf_rsrc(a.table, (uint32_t)((long)a.B * a.MP * 4));
 
     int ib, it, in, ipg;       // the issuing side's window
@@ -695,14 +699,17 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
             }
         }
         const int jl = j & 63;
-        const int b = __builtin_amdgcn_readlane(ib, jl), t0 = __builtin_amdgcn_readlane(it, jl);
+        const int vb = __builtin_amdgcn_readlane(ib, jl), t0 = __builtin_amdgcn_readlane(it, jl);
+        const int b = vb / NG, gh = (vb % NG) * NWV + g;  // sequence, kv head
+        const char* Kg = reinterpret_cast<const char*>(a.Kc) + (long)gh * D * 2;
+        const char* Vg = reinterpret_cast<const char*>(a.Vc) + (long)gh * D * 2;
         // Tiles past the table read pool page 0 (their window entry is a stand-in).
         const int page = (t0 >> a.pshift) < a.MP ? __builtin_amdgcn_readlane(ipg, jl) : 0;
         const bool ok = page >= 0 && page < a.NP;  // outside the pool: zeros
         const long shift = ((long)(ok ? page : 0) * a.P + (t0 & (a.P - 1))) * tok_bytes;
         const uint32_t range = ok ? (uint32_t)(TT * tok_bytes) : 0u;
         const i32x4 rk = buf_rsrc(Kg + shift, range), rv = buf_rsrc(Vg + shift, range);
-        const i32x4 rq = buf_rsrc(a.Q + ((long)b * a.H + g * QPG) * D, (uint32_t)Gm::QB);
+        const i32x4 rq = buf_rsrc(a.Q + ((long)b * a.H + gh * QPG) * D, (uint32_t)Gm::QB);
         const uint32_t sk = ring0 + (j % STG) * WSTAGE, sv = sk + TILE, sq = sv + TILE;
 #pragma unroll
         for (int q = 0; q < NLD; q++) {
@@ -749,7 +756,7 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
         else
             for (int x = wlo; x < w; x = ds_next(x, U, W)) p++;
         const int slot = lo <= u0 ? 0 : 1;
-        float* pe = a.part + ds_state(b, g, p, w, slot, a.B, a.G) * Gm::ST + col * (4 + D);
+        float* pe = a.part + ds_state(b, g, p, w, slot, VB, NWV) * Gm::ST + col * (4 + D);
         if (col < QPG) {
             if (grp == 0) *reinterpret_cast<float4v*>(pe) = float4v{sm, sl, 0.0f, 0.0f};
 #pragma unroll
@@ -768,7 +775,7 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
         l += xor32(l);
         if (pre[b] >= u0) {
             if (col < QPG) {
-                u16* o = a.O + ((long)b * a.H + g * QPG + col) * D + 4 * grp;
+                u16* o = a.O + ((long)(b / NG) * a.H + ((b % NG) * NWV + g) * QPG + col) * D + 4 * grp;
 #pragma unroll
                 for (int dt = 0; dt < D / 16; dt++) {
                     half4 h;
@@ -858,7 +865,7 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
     // The last sequence: finished here when it began in this range and ends
     // with it, else a state.
     if (held) {  // the range's first sequence (it holds unit u0)
-        int bl = 0, bh = a.B - 1;
+        int bl = 0, bh = VB - 1;
         while (bl < bh) {
             const int mid = (bl + bh + 1) >> 1;
             if (pre[mid] <= u0) bl = mid;
@@ -880,10 +887,11 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
 // owns 8 consecutive d of one query head. The first DS_PM pieces' states are
 // read together with the unit prefix (one memory round trip); more pieces
 // follow in batches of 8 ranges.
-template <int D, int QPG>
+template <int D, int QPG, int NWV>
 __global__ __launch_bounds__(64) void decode_stream_merge(DecArgs a, int W) {
     constexpr int ST = DsGeom<D, QPG>::ST, NE = QPG * D / 8;
-    const int b = blockIdx.x / a.G, g = blockIdx.x % a.G, lane = threadIdx.x;
+    const int b = blockIdx.x / NWV, g = blockIdx.x % NWV, lane = threadIdx.x;  // virtual sequence, its head
+    const int VB = a.B * a.NG;
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(a.part, 0, 0x7fffffff, 0x00020000);
     for (int e0 = 0; e0 < NE; e0 += 64) {
         const int e = min(e0 + lane, NE - 1), h = e / (D / 8), d0 = (e % (D / 8)) * 8;
@@ -896,8 +904,8 @@ __global__ __launch_bounds__(64) void decode_stream_merge(DecArgs a, int W) {
         float2v ml[DS_PM];
         float4v x0[DS_PM], x1[DS_PM];
 #pragma unroll
-        for (int p = 0; p < DS_PM; p++) load(ds_state(b, g, p, 0, 0, a.B, a.G), ml[p], x0[p], x1[p]);
-        const int U = a.pre[a.B], lo = a.pre[b], hi = a.pre[b + 1];
+        for (int p = 0; p < DS_PM; p++) load(ds_state(b, g, p, 0, 0, VB, NWV), ml[p], x0[p], x1[p]);
+        const int U = a.pre[VB], lo = a.pre[b], hi = a.pre[b + 1];
         if (hi <= lo) return;  // lens 0: written by decode_stream
         const int wlo = ds_owner(lo, U, W), whi = ds_owner(hi - 1, U, W);
         if (wlo == whi) return;  // finished by its range
@@ -941,7 +949,7 @@ __global__ __launch_bounds__(64) void decode_stream_merge(DecArgs a, int W) {
 #pragma unroll
                 for (int p = 0; p < DS_PM; p++) {
                     const int wq = min(wn, whi);
-                    load(ds_state(b, g, DS_PM, wq, 0, a.B, a.G), ml[p], x0[p], x1[p]);
+                    load(ds_state(b, g, DS_PM, wq, 0, VB, NWV), ml[p], x0[p], x1[p]);
                     if (p0 + p + 1 < np) wn = ds_next(wn, U, W);
                 }
                 fold(min(np - p0, DS_PM));
@@ -951,7 +959,7 @@ __global__ __launch_bounds__(64) void decode_stream_merge(DecArgs a, int W) {
             half8 o;
 #pragma unroll
             for (int q = 0; q < 8; q++) o[q] = (half_t)(A[q] / L);
-            *reinterpret_cast<half8*>(a.O + ((long)b * a.H + g * QPG + h) * D + d0) = o;
+            *reinterpret_cast<half8*>(a.O + ((long)(b / a.NG) * a.H + ((b % a.NG) * NWV + g) * QPG + h) * D + d0) = o;
         }
     }
 }
@@ -959,12 +967,16 @@ __global__ __launch_bounds__(64) void decode_stream_merge(DecArgs a, int W) {
 // Persistent workgroups of the stream path: one per CU.
 int stream_groups() { return num_cus(); }
 
-// Bytes of the stream path's range states: DS_PM per (b, g), then two per
-// (range, g) (ds_state).
+// Wavefronts (kv heads) per workgroup of the balanced path: 4 kv heads, or
+// 8 at a time of a multiple of 8 (0: not this path).
+int64_t stream_nwv(int64_t G) { return G == 4 ? 4 : G > 0 && G % 8 == 0 ? 8 : 0; }
+
+// Bytes of the stream path's range states: DS_PM per (virtual sequence,
+// wavefront), then two per (range, wavefront) (ds_state).
 size_t stream_state_bytes(const TslKernel& k) {
     const int64_t H = k.dim("H"), G = k.name == "paged_attention" ? H : k.dim("G");
-    const int64_t st = (H / G) * (4 + k.dim("D")) * 4;
-    return (size_t)((DS_PM * k.dim("B") * G + (int64_t)stream_groups() * 2 * G) * st);
+    const int64_t st = (H / G) * (4 + k.dim("D")) * 4, nwv = stream_nwv(G);
+    return (size_t)((DS_PM * k.dim("B") * G + (int64_t)stream_groups() * 2 * nwv) * st);
 }
 
 template <int D, int QPG, int NWV>
@@ -977,21 +989,25 @@ int run_decode_stream(DecArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((decode_stream<D, QPG, NWV, STG>), dim3(W), dim3(64 * NWV), 0, s, a);
     int r = TSL_LAUNCHED("decode_attention");
     if (r) return r;
-    hipLaunchKernelGGL((decode_stream_merge<D, QPG>), dim3(a.B * a.G), dim3(64), 0, s, a, W);
+    hipLaunchKernelGGL((decode_stream_merge<D, QPG, NWV>), dim3(a.B * a.NG * NWV), dim3(64), 0, s, a, W);
     return TSL_LAUNCHED("decode_attention merge");
     }
 }
 
 template <int D>
 int run_stream_d(DecArgs& a, int qpg, hipStream_t s) {
-    if (a.G == 8) {
+    if (a.G % 8 == 0) {
+        a.NG = a.G / 8;
         switch (qpg) {
+            case 1: return run_decode_stream<D, 1, 8>(a, s);
             case 2: return run_decode_stream<D, 2, 8>(a, s);
             case 4: return run_decode_stream<D, 4, 8>(a, s);
             case 8: return run_decode_stream<D, 8, 8>(a, s);
         }
     } else {
+        a.NG = 1;
         switch (qpg) {
+            case 1: return run_decode_stream<D, 1, 4>(a, s);
             case 2: return run_decode_stream<D, 2, 4>(a, s);
             case 4: return run_decode_stream<D, 4, 4>(a, s);
             case 8: return run_decode_stream<D, 8, 4>(a, s);
@@ -1034,15 +1050,16 @@ int run_tiles_d(DecArgs& a, int qpg, hipStream_t s) {
 
 bool tiles_path(int64_t D, int64_t P) { return (D == 64 || D == 128) && P % TT == 0; }
 
-// The balanced path: matrix-core shapes with 4 or 8 kv heads (a wavefront
-// each), 2-8 query heads per kv head, tables longer than one chunk, at most
-// DS_MAX_B sequences and 32-bit flat table offsets.
+// The balanced path: matrix-core shapes with 4 or a multiple of 8 kv heads
+// (a wavefront each, 8 at a time), 1-8 query heads per kv head, tables
+// longer than one chunk, at most DS_MAX_B (sequence, head group) pairs and
+// 32-bit flat table offsets.
 bool stream_path(const TslKernel& k) {
     const int64_t H = k.dim("H"), G = k.name == "paged_attention" ? H : k.dim("G");
-    const int64_t qpg = G > 0 ? H / G : 0;
-    return tiles_path(k.dim("D"), k.dim("P")) && (G == 4 || G == 8) && (qpg == 2 || qpg == 4 || qpg == 8) &&
-           ds_stages((int)k.dim("D"), (int)qpg, (int)G) > 0 &&
-           k.dim("MP") > DEC_WIDE_MAX_PAGES && k.dim("B") <= DS_MAX_B && k.dim("B") * k.dim("MP") * 4 < (1LL << 32);
+    const int64_t qpg = G > 0 ? H / G : 0, nwv = stream_nwv(G);
+    return tiles_path(k.dim("D"), k.dim("P")) && nwv > 0 && (qpg == 1 || qpg == 2 || qpg == 4 || qpg == 8) &&
+           ds_stages((int)k.dim("D"), (int)qpg, (int)nwv) > 0 && k.dim("MP") > DEC_WIDE_MAX_PAGES &&
+           k.dim("B") * (G / nwv) <= DS_MAX_B && k.dim("B") * k.dim("MP") * 4 < (1LL << 32);
 }
 
 template <int D, int QPG>
@@ -1098,7 +1115,7 @@ int prepare_decode(TslKernel& k) {
     if (qpg != 1 && qpg != 2 && qpg != 4 && qpg != 8 && qpg != 16)
         return tsl_fail(-2, k.name + ": H / G must be 1, 2, 4, 8 or 16");
     if (stream_path(k)) {  // range states, then the [B + 1] unit prefix
-        size_t bytes = stream_state_bytes(k) + (size_t)(k.dim("B") + 1) * 4;
+        size_t bytes = stream_state_bytes(k) + (size_t)(k.dim("B") * (G / stream_nwv(G)) + 1) * 4;
         if (tsl_hip_check(hipMalloc(&k.scratch, bytes), "decode_attention scratch")) return -1;
         k.scratch_bytes = bytes;
         return 0;

@@ -246,6 +246,19 @@ def test_paged_attention_reference_case():
     assert_close("paged vs f64", got, paged_ref(q, kc, vc, table, lens, scale), 3e-3)
 
 
+@pytest.mark.parametrize("b,h,d,p,lo,hi", [(6, 16, 64, 16, 1, 2000), (3, 32, 128, 32, 0, 4000), (5, 8, 128, 16, 900, 1500)])
+def test_paged_attention_long_tables(b, h, d, p, lo, hi):
+    # paged_attention (G = H) with tables longer than 64 pages: the balanced
+    # form, 8 heads at a time (16 and 32 heads) or all 8, one query head each.
+    _say("paged long", b, h, d, p)
+    q, kc, vc, table, lens, scale = decode_case(9 + b, b=b, h=h, g=h, d=d, p=p, lo=lo, hi=hi,
+                                                mp=max(65, (hi + p - 1) // p))
+    want = oracle.decode_attention(q, kc, vc, table, lens, scale, threads=8)
+    got = T.run("attention", "paged_attention", [q, kc, vc, table, lens, np.zeros_like(q)], [T.F32(scale)],
+                outputs=[5])[5]
+    parity("paged long", got, want)
+
+
 def decode_case(seed, b=64, h=32, g=8, d=128, p=16, lo=128, hi=4096, mp=None):
     """lens ~ U[lo, hi], pages assigned by a seeded
     permutation into int32 block tables, KV pool N(0,1) f16."""
@@ -283,7 +296,10 @@ def _decode(q, kc, vc, table, lens, scale):
                                  dict(b=1, h=32, g=8, d=128, p=16, lo=1100, hi=1100),
                                  dict(b=40, h=32, g=8, d=64, p=16, lo=0, hi=40, mp=80),
                                  dict(b=3, h=16, g=4, d=128, p=64, lo=1, hi=9000),
-                                 dict(b=17, h=32, g=4, d=128, p=16, lo=2000, hi=5000)])
+                                 dict(b=17, h=32, g=4, d=128, p=16, lo=2000, hi=5000),
+                                 # 16 and 32 kv heads: 8 at a time (head groups as sequences of their own)
+                                 dict(b=5, h=32, g=16, d=128, p=16, lo=100, hi=3000),
+                                 dict(b=3, h=32, g=32, d=64, p=32, lo=0, hi=4000)])
 def test_decode_attention_vs_oracle(cfg):
     _say("decode", cfg)
     q, kc, vc, table, lens, scale = decode_case(1, **cfg)
