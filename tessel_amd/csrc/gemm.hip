@@ -721,7 +721,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const u16* __restri
 // EPI_ROPE pairs rows the same way inside W: block b holds rotary pairs
 // 8 b .. 8 b + 7 (pair p: column h D + i and its partner h D + D2 + i, with
 // h = p / D2, i = p % D2), so N counts pairs and the epilogue rotates them.
-constexpr int SL_KS = 2048;
+constexpr int SL_KS = 2816;  // 22 x 128: K = 5632 in two slices (256 workgroups at N = 2048, one round)
 
 // Rotary pair n of token m from its two projection sums: QKV's f16 rounding,
 // then llm.tl rope_q (query heads) or kv_write (key heads rotated, value
@@ -778,7 +778,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     constexpr int WB = 16 * SL_KS * 2;           // LDS bytes of the W block
     constexpr int XS = 16 * MT * 128;            // LDS bytes of one X step
     constexpr int XD = sl_xdepth<MT>();          // X stages per wavefront
-    constexpr int MAXU = SL_KS / 64 / SK_WAVES;  // k steps per wavefront
+    constexpr int MAXU = (SL_KS / 64 + SK_WAVES - 1) / SK_WAVES;  // k steps per wavefront, at most
     constexpr int XL = 2 * MT;                   // X loads per step (8 rows each)
     __shared__ __attribute__((aligned(16))) u16 lds[(WB + SK_WAVES * XD * XS) / 2];
     __shared__ float red[SK_WAVES][4][64];
