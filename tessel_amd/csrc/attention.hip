@@ -185,6 +185,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
     float m = PREFILL ? -1e30f : -INFINITY;  // running max of raw scores
     float mc = PREFILL ? -1e30f * c2 : -INFINITY;  // the same, times c2
     float lsum = 0.0f;
+    bool have_m = false;  // a block's max has set m
     float16v acc[DP / 32];
 #pragma unroll
     for (int i = 0; i < DP / 32; i++) acc[i] = float16v{};
@@ -230,37 +231,56 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
                     st[kt][r] = keep ? st[kt][r] : -INFINITY;
                 }
         }
-        float mb = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) mb = fmaxf(mb, st[kt][r]);
-        mb = fmaxf(mb, xor32(mb));
-        // Lazy rescaling: the running max moves only when it would grow by
-        // more than 2^LAZY (p stays <= 2^LAZY meanwhile; acc / l does not
-        // depend on which max was used).
-        const bool grow = mb * c2 > mc + LAZY;
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-            const float mn = fmaxf(m, mb);
-            const float mcn = mn * c2;
-            const float alpha = __builtin_amdgcn_exp2f(mc - mcn);
-            lsum *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < DP / 32; dt++) acc[dt] *= alpha;
-            m = mn;
-            mc = mcn;
-        }
         // P = exp2(s c2 - m c2), rounded to f16 as the .tl's f16(p); row sums
         // from the f16 pairs. Then O^T += V^T P^T over the block's 4 k-steps.
         half8 pk[4];
+        auto exps = [&]() {
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+            for (int t = 0; t < 4; t++) {
 #pragma unroll
-            for (int hh = 0; hh < 8; hh++)
-                pk[t][hh] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(st[t >> 1][8 * (t & 1) + hh], c2, -mc));
+                for (int hh = 0; hh < 8; hh++)
+                    pk[t][hh] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(st[t >> 1][8 * (t & 1) + hh], c2, -mc));
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                lsum = __builtin_amdgcn_fdot2(half2v{pk[t][2 * e], pk[t][2 * e + 1]}, ones, lsum, false);
+                for (int e = 0; e < 4; e++)
+                    lsum = __builtin_amdgcn_fdot2(half2v{pk[t][2 * e], pk[t][2 * e + 1]}, ones, lsum, false);
+            }
+        };
+        // The running max is taken from the scores only when it must move:
+        // p is exponentiated against the current one, and only a score that
+        // outgrew it by 2^16 (an f16 p, and so the row sum, infinite) sends
+        // the block back through the max below. The first block always goes
+        // there. acc / l does not depend on which max was used.
+        bool redo = !have_m;
+        if (have_m) {
+            const float l0 = lsum;
+            exps();
+            if (__builtin_amdgcn_ballot_w64(__builtin_isinf(lsum)) != 0) {
+                lsum = l0;
+                redo = true;
+            }
+        }
+        if (redo) {
+            float mb = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) mb = fmaxf(mb, st[kt][r]);
+            mb = fmaxf(mb, xor32(mb));
+            // Lazy rescaling: the running max moves only when it would grow
+            // by more than 2^LAZY.
+            const bool grow = mb * c2 > mc + LAZY;
+            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+                const float mn = fmaxf(m, mb);
+                const float mcn = mn * c2;
+                const float alpha = __builtin_amdgcn_exp2f(mc - mcn);
+                lsum *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < DP / 32; dt++) acc[dt] *= alpha;
+                m = mn;
+                mc = mcn;
+            }
+            have_m = true;
+            exps();
         }
 #pragma unroll
         for (int dt = 0; dt < DP / 32; dt++) {

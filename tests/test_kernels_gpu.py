@@ -197,6 +197,31 @@ def test_flash_attention_baseline_shapes(s):
     parity("flash baseline", got, want)
 
 
+@pytest.mark.parametrize("name", ["flash_attention", "prefill_attention"])
+@pytest.mark.parametrize("s", [300, 2000])
+def test_attention_scores_that_outgrow_the_running_max(name, s):
+    # Keys of later blocks scaled up 12x (scores jump by far more than 2^16
+    # in the exp2 domain): p against the stale running max overflows f16, and
+    # the block is redone through its max. Short and long sequences (both
+    # key-split forms), plain and prefill (GQA, two packed prompts).
+    _say("attention growth", name, s)
+    rng = np.random.default_rng(s + 7)
+    if name == "flash_attention":
+        q, k, v = (rng.standard_normal((4, s, 64)).astype(np.float16) for _ in range(3))
+        k[:, s // 3:s // 3 + 40] *= np.float16(12)
+        k[:, 2 * s // 3:] *= np.float16(3)
+        want = oracle.flash_attention(q, k, v, 0.125, threads=8)
+        got = T.run("attention", name, [q, k, v, np.zeros_like(q)], [T.F32(0.125)], outputs=[3])[3]
+    else:
+        q = rng.standard_normal((s, 8, 64)).astype(np.float16)
+        k, v = (rng.standard_normal((s, 2, 64)).astype(np.float16) for _ in range(2))
+        k[s // 3:s // 3 + 40] *= np.float16(12)
+        starts = np.where(np.arange(s) < s // 2, 0, s // 2).astype(np.int32)
+        want = oracle.prefill_attention(q, k, v, starts, 0.125, threads=8)
+        got = T.run("llm", name, [q, k, v, starts, np.zeros_like(q)], [T.F32(0.125)], outputs=[4])[4]
+    parity("attention growth", got, want)
+
+
 @pytest.mark.parametrize("s", [2048, 4096])
 def test_flash_attention_long_sampled(s):
     # Long sequences: sampled query rows against the f64 closed form
