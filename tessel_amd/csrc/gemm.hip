@@ -725,44 +725,43 @@ constexpr int SL_KS = 2816;  // 22 x 128: K = 5632 in two slices (256 workgroups
 
 // Rotary pair n of token m from its two projection sums: QKV's f16 rounding,
 // then llm.tl rope_q (query heads) or kv_write (key heads rotated, value
-// heads copied; both also into the paged cache at slot[m] when it is in
-// [0, NS)), with the arithmetic of rope_q_elem / kv_write_elem.
-TSL_DEV void rope_store(const RopeEpi& ep, int m, int n, float v1, float v2) {
-    const int h = n / ep.D2, i = n % ep.D2;
+// heads copied), with the arithmetic of rope_q_elem / kv_write_elem (c, s
+// from rope_cs); y1 goes to column n % D2 of its head, y2 to column
+// D2 + n % D2.
+// The rotation's cos and sin for pair n at position p (zeros outside the
+// tables; value heads are not rotated).
+TSL_DEV void rope_cs(const RopeEpi& ep, int p, int n, float& c, float& s) {
+    const bool use = n / ep.D2 < ep.H + ep.G && p >= 0 && p < ep.NPOS;
+    const int i = n % ep.D2;
+    c = use ? ep.Cs[(size_t)p * ep.D2 + i] : 0.0f;
+    s = use ? ep.Sn[(size_t)p * ep.D2 + i] : 0.0f;
+}
+TSL_DEV void rope_pair(const RopeEpi& ep, int n, float v1, float v2, float c, float s, u16& y1, u16& y2) {
+    const int h = n / ep.D2;
     const u16 b1 = f2h(v1), b2 = f2h(v2);
-    const float x1 = h2f(b1), x2 = h2f(b2);
-    const int p = ep.pos[m];
-    const bool pin = p >= 0 && p < ep.NPOS;
     if (h < ep.H + ep.G) {
-        const float c = pin ? ep.Cs[(size_t)p * ep.D2 + i] : 0.0f, s = pin ? ep.Sn[(size_t)p * ep.D2 + i] : 0.0f;
-        u16 y1, y2;
-        rope_rotate(x1, x2, c, s, y1, y2);
-        if (h < ep.H) {
-            u16* q = ep.Q + ((size_t)m * ep.H + h) * ep.D;
-            q[i] = y1;
-            q[ep.D2 + i] = y2;
-            return;
-        }
-        const int g = h - ep.H, at = ep.slot[m];
-        u16* kk = ep.K + ((size_t)m * ep.G + g) * ep.D;
-        kk[i] = y1;
-        kk[ep.D2 + i] = y2;
-        if (at >= 0 && at < ep.NS) {
-            u16* kc = ep.Kc + ((size_t)at * ep.G + g) * ep.D;
-            kc[i] = y1;
-            kc[ep.D2 + i] = y2;
-        }
+        rope_rotate(h2f(b1), h2f(b2), c, s, y1, y2);
+    } else {
+        y1 = b1;
+        y2 = b2;
+    }
+}
+
+// The 16 rotated halves of a block (8 pairs of head h from column i0) for
+// token m, as two 16-byte runs: Q rows, or K / V rows and the paged cache at
+// slot[m] when it is in [0, NS).
+TSL_DEV void rope_row_store(const RopeEpi& ep, int m, int h, int i0, int half, int at, u32x4 v) {
+    const int c = half * ep.D2 + i0;
+    if (h < ep.H) {
+        *reinterpret_cast<u32x4*>(ep.Q + ((size_t)m * ep.H + h) * ep.D + c) = v;
         return;
     }
-    const int g = h - ep.H - ep.G, at = ep.slot[m];
-    u16* vv = ep.V + ((size_t)m * ep.G + g) * ep.D;
-    vv[i] = b1;
-    vv[ep.D2 + i] = b2;
-    if (at >= 0 && at < ep.NS) {
-        u16* vc = ep.Vc + ((size_t)at * ep.G + g) * ep.D;
-        vc[i] = b1;
-        vc[ep.D2 + i] = b2;
-    }
+    const bool key = h < ep.H + ep.G;
+    const int g = key ? h - ep.H : h - ep.H - ep.G;
+    u16* row = key ? ep.K : ep.V;
+    u16* cache = key ? ep.Kc : ep.Vc;
+    *reinterpret_cast<u32x4*>(row + ((size_t)m * ep.G + g) * ep.D + c) = v;
+    if (at >= 0 && at < ep.NS) *reinterpret_cast<u32x4*>(cache + ((size_t)at * ep.G + g) * ep.D + c) = v;
 }
 
 template <int MT>
@@ -781,7 +780,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     constexpr int MAXU = (SL_KS / 64 + SK_WAVES - 1) / SK_WAVES;  // k steps per wavefront, at most
     constexpr int XL = 2 * MT;                   // X loads per step (8 rows each)
     __shared__ __attribute__((aligned(16))) u16 lds[(WB + SK_WAVES * XD * XS) / 2];
-    __shared__ float red[SK_WAVES][4][64];
+    __shared__ __attribute__((aligned(16))) float red[SK_WAVES][4][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row = lane & 15, g = lane >> 4;
@@ -792,6 +791,18 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     const int k0 = 128 * b0, KS = 128 * (b1 - b0), cpr = KS / 8, nst = KS / 64;
     const uint32_t lds_w = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
     const uint32_t lds_x = lds_w + WB + wave * XD * XS;
+    // The rotary epilogue's positions and cache slots, loaded before the
+    // stream; its cos and sin follow after the k loop, behind the
+    // reduction's barriers.
+    int rpos[ROPE ? MT : 1], rslot = -1;
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int m = 16 * t + (lane & 15);
+            rpos[t] = tid < 256 && m < M ? ep.pos[m] : -1;
+        }
+        if (tid < 2 * M) rslot = ep.slot[tid >> 1];  // the write-out's row
+    }
 
     // W block: 16 cpr chunks; load q covers linear chunks 64 q .. 64 q + 63
     // (row p / cpr, position p % cpr). Rows past N read as zero.
@@ -872,6 +883,12 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
     }
+    float rc[ROPE ? MT : 1], rsn[ROPE ? MT : 1];
+    if constexpr (ROPE) {
+        const int n = n0 + 4 * ((tid & 63) >> 4) + (tid >> 6);
+#pragma unroll
+        for (int t = 0; t < MT; t++) rope_cs(ep, rpos[t], n, rc[t], rsn[t]);
+    }
     // Sum the 8 partial tiles through LDS in wavefront order; thread tid < 256
     // keeps element tid (register tid/64 of lane tid%64) of each.
     float sum[MT];
@@ -900,6 +917,32 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
             __syncthreads();
             up[t] = tid < 256 && l < 32 ? red[0][r][l + 32] : 0.0f;
         }
+    }
+    if constexpr (ROPE) {
+        // The block's 8 pairs lie in one head (D2 % 8 == 0): the rotated
+        // halves go through LDS, then each token row leaves as two 16-byte
+        // stores (per element 2-byte stores would scatter over 16 rows).
+        static_assert(16 * MT * 16 * 2 <= (int)sizeof(red), "staging fits the reduction buffer");
+        u16 (*yb)[16] = reinterpret_cast<u16 (*)[16]>(&red[0][0][0]);  // [16 MT][16]
+        __syncthreads();  // the exchange above has read red
+        if (tid < 256 && l < 32) {
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int pl = 4 * (l >> 4) + r, m = 16 * t + (l & 15);
+                if (m >= M || n0 + pl >= N) continue;
+                u16 y1, y2;
+                rope_pair(ep, n0 + pl, sum[t], up[t], rc[t], rsn[t], y1, y2);
+                yb[m][pl] = y1;
+                yb[m][8 + pl] = y2;
+            }
+        }
+        __syncthreads();
+        const int h = n0 / ep.D2, i0 = n0 % ep.D2;
+        if (tid < 2 * M)  // M <= 64: one row half per thread
+            rope_row_store(ep, tid >> 1, h, i0, tid & 1, rslot, *reinterpret_cast<const u32x4*>(&yb[tid >> 1][8 * (tid & 1)]));
+        return;
+    }
+    if constexpr (DUAL) {
         if (l >= 32) return;
     }
     if (tid >= 256) return;
@@ -908,10 +951,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         const int n = n0 + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
         if (m >= M || n >= N) continue;
         const float v = sum[t], uu = DUAL ? up[t] : 0.0f;
-        if constexpr (ROPE) {
-            rope_store(ep, m, n, v, uu);
-            continue;
-        }
         if constexpr (SPLIT) {
             float* pp = part + (size_t)ks * (DUAL ? 2 : 1) * M * N + (size_t)m * N + n;
             pp[0] = v;
