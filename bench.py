@@ -197,14 +197,51 @@ PROJ = (("linear", 2048, 2560, "qkv"), ("linear_residual", 2048, 2048, "o"), ("g
         ("linear_residual", 5632, 2048, "down"), ("logits", 2048, 32000, "logits"))
 
 
+class RotTimed(Timed):
+    """Timed launches that cycle through several argument lists (weight
+    copies whose total exceeds the 256 MB last-level cache, so every launch
+    streams its weights from HBM, as the engine's 22 layers do)."""
+
+    def __init__(self, T, k, arg_sets):
+        super().__init__(T, k, arg_sets[0])
+        self.sets, self.i = arg_sets, 0
+
+    def _next(self):
+        self.i = (self.i + 1) % len(self.sets)
+        return self.sets[self.i]
+
+    def _warm(self, seconds, min_launches):
+        T = self.T
+        t0, n = time.perf_counter(), 0
+        while n < min_launches or time.perf_counter() - t0 < seconds:
+            T.launch(self.k, self._next())
+            n += 1
+            if n % 8 == 0:
+                T.sync()
+        T.sync()
+
+    def run(self, iters):
+        T = self.T
+        T.sync()
+        a = T.event_record()
+        for _ in range(iters):
+            T.launch(self.k, self._next())
+        b = T.event_record()
+        T.sync()
+        return T.event_elapsed(a, b) / iters
+
+
 def proj_case(T, name, m, k, n, seed=6):
     """One kernels/llm.tl projection X[m, k] W^T. Returns the timer, its
     flops and the HBM bytes it must move (weights once, X, Y, and R read and
-    written for linear_residual)."""
+    written for linear_residual). Decode-sized (m <= 64) products cycle
+    through weight copies totalling more than 512 MB, so the weights come
+    from HBM and not from the last-level cache."""
     rng = np.random.default_rng(seed)
     x = f16(rng.standard_normal((m, k), np.float32))
     ws = [f16(rng.standard_normal((n, k), np.float32) / np.float32(np.sqrt(k)))
           for _ in range(2 if name == "gate_up" else 1)]
+    copies = max(1, -(-(512 << 20) // sum(w.nbytes for w in ws))) if m <= 64 else 1
     if name == "linear_residual":
         y = T.tensor(np.zeros((m, n), np.float32))
         ybytes = 8 * m * n
@@ -214,11 +251,14 @@ def proj_case(T, name, m, k, n, seed=6):
     else:
         y = T.alloc(2 * m * n)
         ybytes = 2 * m * n
-    bufs = [T.tensor(x)] + [T.tensor(w) for w in ws] + [y]
+    xb = T.tensor(x)
+    wbs = [[T.tensor(w) for w in ws] for _ in range(copies)]
     kern = T.kernel("llm", name, [x.shape] + [w.shape for w in ws] + [(m, n)])
     flops = 2.0 * m * n * k * len(ws)
     nbytes = 2.0 * n * k * len(ws) + 2.0 * m * k + ybytes
-    return Timed(T, kern, bufs), flops, nbytes
+    if copies == 1:
+        return Timed(T, kern, [xb] + wbs[0] + [y]), flops, nbytes
+    return RotTimed(T, kern, [[xb] + wb + [y] for wb in wbs]), flops, nbytes
 
 
 def paged_case(T, seed=3, b=16, h=32, d=128, p=16):
