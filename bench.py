@@ -162,41 +162,6 @@ def decode_case(T, seed=2, b=64, h=32, g=8, d=128, p=16):
     return Timed(T, kern, bufs), nbytes, flops, int(lens.sum())
 
 
-def rows_case(T, kind):
-    rng = np.random.default_rng(3)
-    r = c = 4096
-    if kind == "softmax":
-        x = (rng.random((r, c), np.float32) * 8 - 4).astype(np.float32)
-        bufs = [T.tensor(x), T.alloc(r * c * 4)]
-        k = T.kernel("basic", "softmax", [[r, c]] * 2, [("BR", 1), ("BC", c)])
-        return Timed(T, k, bufs), 8.0 * r * c
-    x = f16(rng.random((r, c), np.float32) * 4 - 2)
-    w = f16(rng.random(c, np.float32) * 2 - 1)
-    bufs = [T.tensor(x), T.tensor(w), T.alloc(r * c * 2), T.F32(1e-5)]
-    k = T.kernel("basic", "rmsnorm", [[r, c], [c], [r, c]], [("BR", 1), ("BC", c)])
-    return Timed(T, k, bufs), 4.0 * r * c
-
-
-def prefill_case(T, seed=4, lens=(512, 512), h=32, g=4, d=64):
-    """kernels/llm.tl prefill_attention at the engine's prefill step
-    (BASELINE config 5: two 512-token prompts packed into 1024 rows)."""
-    rng = np.random.default_rng(seed)
-    t = sum(lens)
-    q = f16(rng.standard_normal((t, h, d), np.float32))
-    k, v = (f16(rng.standard_normal((t, g, d), np.float32)) for _ in range(2))
-    starts = np.concatenate([np.full(l, sum(lens[:i]), np.int32) for i, l in enumerate(lens)])
-    bufs = [T.tensor(q), T.tensor(k), T.tensor(v), T.tensor(starts), T.alloc(q.nbytes), T.F32(1.0 / np.sqrt(d))]
-    kern = T.kernel("llm", "prefill_attention", [q.shape, k.shape, v.shape, starts.shape, q.shape])
-    flops = sum(2.0 * h * l * l * d for l in lens)  # the causal half of 4 H L^2 D per prompt
-    return Timed(T, kern, bufs), flops
-
-
-# The TinyLlama projections (BASELINE config 5: dim 2048, QKV 2560, FFN 5632,
-# vocab 32000) as the engine runs them: name, K, N.
-PROJ = (("linear", 2048, 2560, "qkv"), ("linear_residual", 2048, 2048, "o"), ("gate_up", 2048, 5632, "gate_up"),
-        ("linear_residual", 5632, 2048, "down"), ("logits", 2048, 32000, "logits"))
-
-
 class RotTimed(Timed):
     """Timed launches that cycle through several argument lists (weight
     copies whose total exceeds the 256 MB last-level cache, so every launch
@@ -229,6 +194,44 @@ class RotTimed(Timed):
         b = T.event_record()
         T.sync()
         return T.event_elapsed(a, b) / iters
+
+
+def rows_case(T, kind):
+    """basic.softmax / basic.rmsnorm over 4096^2, cycling through input and
+    output copies totalling 512 MB or more, so rows come from HBM and not from
+    the 256 MB last-level cache."""
+    rng = np.random.default_rng(3)
+    r = c = 4096
+    if kind == "softmax":
+        x = (rng.random((r, c), np.float32) * 8 - 4).astype(np.float32)
+        k = T.kernel("basic", "softmax", [[r, c]] * 2, [("BR", 1), ("BC", c)])
+        sets = [[T.tensor(x), T.alloc(r * c * 4)] for _ in range(4)]
+        return RotTimed(T, k, sets), 8.0 * r * c
+    x = f16(rng.random((r, c), np.float32) * 4 - 2)
+    w = T.tensor(f16(rng.random(c, np.float32) * 2 - 1))
+    k = T.kernel("basic", "rmsnorm", [[r, c], [c], [r, c]], [("BR", 1), ("BC", c)])
+    sets = [[T.tensor(x), w, T.alloc(r * c * 2), T.F32(1e-5)] for _ in range(8)]
+    return RotTimed(T, k, sets), 4.0 * r * c
+
+
+def prefill_case(T, seed=4, lens=(512, 512), h=32, g=4, d=64):
+    """kernels/llm.tl prefill_attention at the engine's prefill step
+    (BASELINE config 5: two 512-token prompts packed into 1024 rows)."""
+    rng = np.random.default_rng(seed)
+    t = sum(lens)
+    q = f16(rng.standard_normal((t, h, d), np.float32))
+    k, v = (f16(rng.standard_normal((t, g, d), np.float32)) for _ in range(2))
+    starts = np.concatenate([np.full(l, sum(lens[:i]), np.int32) for i, l in enumerate(lens)])
+    bufs = [T.tensor(q), T.tensor(k), T.tensor(v), T.tensor(starts), T.alloc(q.nbytes), T.F32(1.0 / np.sqrt(d))]
+    kern = T.kernel("llm", "prefill_attention", [q.shape, k.shape, v.shape, starts.shape, q.shape])
+    flops = sum(2.0 * h * l * l * d for l in lens)  # the causal half of 4 H L^2 D per prompt
+    return Timed(T, kern, bufs), flops
+
+
+# The TinyLlama projections (BASELINE config 5: dim 2048, QKV 2560, FFN 5632,
+# vocab 32000) as the engine runs them: name, K, N.
+PROJ = (("linear", 2048, 2560, "qkv"), ("linear_residual", 2048, 2048, "o"), ("gate_up", 2048, 5632, "gate_up"),
+        ("linear_residual", 5632, 2048, "down"), ("logits", 2048, 32000, "logits"))
 
 
 def proj_case(T, name, m, k, n, seed=6):
