@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
         }
         lsum = L;
     }
-    const float l = lsum + xor32(lsum);
+    const DivBy by_l(lsum + xor32(lsum));  // l >= 1: the row's largest p is 1 or more
     if (myq < a.S) {
         u16* o = a.O + (long)myq * a.q_row + (long)h * a.q_head;
 #pragma unroll
@@ -345,10 +345,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
             for (int rg = 0; rg < 4; rg++) {
                 const int d = dt * 32 + 8 * rg + 4 * g4;
                 if (d >= D) continue;
-                uint32_t w0 = (uint32_t)f2h(acc[dt][4 * rg] / l) | ((uint32_t)f2h(acc[dt][4 * rg + 1] / l) << 16);
-                uint32_t w1 = (uint32_t)f2h(acc[dt][4 * rg + 2] / l) | ((uint32_t)f2h(acc[dt][4 * rg + 3] / l) << 16);
-                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-                *reinterpret_cast<u32x2_t*>(o + d) = u32x2_t{w0, w1};
+                const half4 y = {(half_t)by_l(acc[dt][4 * rg]), (half_t)by_l(acc[dt][4 * rg + 1]),
+                                 (half_t)by_l(acc[dt][4 * rg + 2]), (half_t)by_l(acc[dt][4 * rg + 3])};
+                *reinterpret_cast<half4*>(o + d) = y;
             }
     }
 }

@@ -40,6 +40,23 @@ TSL_DEV void rope_rotate(float x1, float x2, float c, float s, u16& y1, u16& y2)
     y2 = f2h(__builtin_fmaf(x2, c, x1 * s));
 }
 
+// x / d for many x and one d (Markstein's method: a reciprocal refined by one
+// Newton step, then one residual correction of each quotient). Three
+// operations per quotient instead of a full IEEE division's ~11; the result is
+// the correctly rounded f32 quotient except in rare near-halfway cases, where it
+// is one ulp off. For d finite, positive and normal.
+struct DivBy {
+    float d, r;
+    TSL_DEV explicit DivBy(float den) : d(den) {
+        const float r0 = __builtin_amdgcn_rcpf(den);
+        r = __builtin_fmaf(__builtin_fmaf(-den, r0, 1.0f), r0, r0);
+    }
+    TSL_DEV float operator()(float x) const {
+        const float q = x * r;
+        return __builtin_fmaf(__builtin_fmaf(-q, d, x), r, q);
+    }
+};
+
 // DPP row operations within 16-lane rows (gfx9 DPP controls).
 template <int CTRL>
 TSL_DEV float dpp(float x) {
