@@ -272,10 +272,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
             if (__builtin_amdgcn_ballot_w64(grow) != 0) {
                 const float mn = fmaxf(m, mb);
                 const float mcn = mn * c2;
-                const float alpha = __builtin_amdgcn_exp2f(mc - mcn);
-                lsum *= alpha;
+                if (have_m) {  // before the first block acc and lsum are zero
+                    const float alpha = __builtin_amdgcn_exp2f(mc - mcn);
+                    lsum *= alpha;
 #pragma unroll
-                for (int dt = 0; dt < DP / 32; dt++) acc[dt] *= alpha;
+                    for (int dt = 0; dt < DP / 32; dt++) acc[dt] *= alpha;
+                }
                 m = mn;
                 mc = mcn;
             }
