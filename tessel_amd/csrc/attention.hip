@@ -73,8 +73,10 @@ TSL_DEV int swz_v(int key) {  // in 16-byte chunks
 // wavefront b % 2, each block with its own LDS stages), so a workgroup's
 // critical path is half its keys; the two states of each row are merged
 // through LDS at the end (max, then the rescaled sums, in wavefront order).
+// D = 128 with the key split holds 4 stages of 32 KB: one workgroup per CU,
+// so its launch bounds ask for one (and the registers that allows).
 template <int D, bool PREFILL, int KS>
-__global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs a) {
+__global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(AttnArgs a) {
     constexpr int DP = D < 32 ? 32 : D;     // V^T rows, padded to one MFMA tile
     constexpr int KCH = D / 8;              // 16-byte chunks per row
     constexpr int ROWB = 2 * D;             // bytes per K or V row
