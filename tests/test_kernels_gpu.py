@@ -174,7 +174,10 @@ def test_split_k_products_repeat_bit_identically():
 
 # ---------------------------------------------------------------- attention
 
-@pytest.mark.parametrize("h,s,d", [(2, 150, 32), (2, 100, 32), (1, 40, 16), (4, 300, 64), (2, 200, 128)])
+# The small cases take the key-split form (at most 256 query blocks x heads);
+# the last two, the unsplit form at D = 128 and D = 32.
+@pytest.mark.parametrize("h,s,d", [(2, 150, 32), (2, 100, 32), (1, 40, 16), (4, 300, 64), (2, 200, 128),
+                                   (32, 1100, 128), (24, 1400, 32)])
 def test_flash_attention_vs_oracle(h, s, d):
     _say("flash", h, s, d)
     r = oracle.Rng(4 + s)
