@@ -14,6 +14,15 @@ namespace {
 
 constexpr int ROWS_PER_WG = 4;  // one wavefront per row, 4 per workgroup
 
+// softmax and basic.rmsnorm rows are read once and their outputs are not
+// read back by the same kernel: nontemporal loads and stores (4096^2, rows
+// from HBM: rmsnorm 14.0 -> 13.2 us, softmax 27.1 -> 25.6 us, with softmax's
+// division as DivBy).
+template <class T>
+TSL_DEV T load_once(const T* p) { return __builtin_nontemporal_load(p); }
+template <class T>
+TSL_DEV void store_out(T v, T* p) { __builtin_nontemporal_store(v, p); }
+
 // ---------------------------------------------------------------- softmax
 // Y[r, c] = exp(x - max) / sum(exp(x - max)) over the first ncols = min(BC, C)
 // columns; columns past C read -inf (kernels/basic.tl:13), so they add 0.
@@ -31,7 +40,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ 
     for (int i = 0; i < NV; i++) {
         const int c = i * 256 + lane * 4;
         if (vec && c + 4 <= ncols) {
-            float4v t = *reinterpret_cast<const float4v*>(x + c);
+            float4v t = load_once(reinterpret_cast<const float4v*>(x + c));
             for (int e = 0; e < 4; e++) v[i][e] = t[e];
         } else {
             for (int e = 0; e < 4; e++) v[i][e] = (c + e < ncols) ? x[c + e] : -INFINITY;
@@ -46,17 +55,17 @@ __global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ 
             v[i][e] = expf(v[i][e] - m);
             s += v[i][e];
         }
-    s = wave_sum(s);
+    const DivBy by_s(wave_sum(s));  // s >= 1: the row's max contributes exp(0)
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int c = i * 256 + lane * 4;
         if (vec && c + 4 <= ncols) {
             float4v t;
-            for (int e = 0; e < 4; e++) t[e] = v[i][e] / s;
-            *reinterpret_cast<float4v*>(y + c) = t;
+            for (int e = 0; e < 4; e++) t[e] = by_s(v[i][e]);
+            store_out(t, reinterpret_cast<float4v*>(y + c));
         } else {
             for (int e = 0; e < 4; e++)
-                if (c + e < ncols) y[c + e] = v[i][e] / s;
+                if (c + e < ncols) y[c + e] = by_s(v[i][e]);
         }
     }
 }
@@ -111,10 +120,10 @@ TSL_DEV void rms_store(const float (&v)[NV][E], float rs, const u16* __restrict_
                 o[p] = (uint32_t)lo | ((uint32_t)hi << 16);
             }
             if constexpr (E == 8) {
-                *reinterpret_cast<u32x4*>(y + c) = u32x4{o[0], o[1], o[2], o[3]};
+                store_out(u32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<u32x4*>(y + c));
             } else {
                 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-                *reinterpret_cast<u32x2*>(y + c) = u32x2{o[0], o[1]};
+                store_out(u32x2{o[0], o[1]}, reinterpret_cast<u32x2*>(y + c));
             }
         } else {
             for (int e = 0; e < E; e++)
@@ -143,10 +152,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ X, 
         const int c = (i * 64 + lane) * E;
         if (rin && vec && c + E <= ncols) {
             if constexpr (sizeof(XT) == 2) {
-                u32x4 t = *reinterpret_cast<const u32x4*>(x + c);
+                u32x4 t = load_once(reinterpret_cast<const u32x4*>(x + c));
                 for (int e = 0; e < E; e++) v[i][e] = h2f((u16)(t[e >> 1] >> (16 * (e & 1))));
             } else {
-                float4v t = *reinterpret_cast<const float4v*>(x + c);
+                float4v t = load_once(reinterpret_cast<const float4v*>(x + c));
                 for (int e = 0; e < E; e++) v[i][e] = t[e];
             }
         } else {
