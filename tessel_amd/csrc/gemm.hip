@@ -819,10 +819,10 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
             const int rr = DUAL ? r & 7 : r;  // row within its matrix
             const uint32_t off = (uint32_t)((rr * K + 8 * (pos ^ (r & 15))) * 2);
             if (DUAL && q * 64 >= 8 * cpr)  // rows 8..15: Wu (uniform: 8 cpr is a multiple of 64)
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_w + q * 1024),
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds_w + q * 1024),
                              "v"(off), "s"(rw2));
             else
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_w + q * 1024),
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds_w + q * 1024),
                              "v"(off), "s"(rw));
         }
     }
@@ -1014,11 +1014,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
             const int rr = DUAL ? r & 7 : r;
             const uint32_t off = (uint32_t)((rr * K + 8 * (pos ^ (r & 15))) * 2);
             if (DUAL && q >= nl / 2)  // rows 8..15: Wu
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(ring + slot * SLOT + q * 1024),
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(ring + slot * SLOT + q * 1024),
                              "v"(off), "s"(rw2)
                              : "memory");
             else
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(ring + slot * SLOT + q * 1024),
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(ring + slot * SLOT + q * 1024),
                              "v"(off), "s"(rw)
                              : "memory");
         }
