@@ -163,7 +163,10 @@ int tsl_engine_step(int engine, int n, const int32_t* tokens, const int32_t* pos
  * stats: prefill_steps, decode_steps, prompt_tokens, generated,
  * largest_batch, decode_tokens (int64) and seconds, decode_seconds.
  * out_times (may be NULL): 2 nreq doubles, request r's Output::first_token_s
- * and done_s (seconds from the start of the call, src/llm/sched.rs:14-20). */
+ * and done_s (seconds from the start of the call, src/llm/sched.rs:14-20).
+ * Every request is checked before any step runs: an empty prompt, one
+ * longer than max_tokens, max_new < 1, or more pages than max_seq_pages or
+ * the whole pool holds is TSL_ERR_ARG. */
 typedef struct {
     int64_t prefill_steps, decode_steps, prompt_tokens, generated, largest_batch, decode_tokens;
     double seconds, decode_seconds;
@@ -171,6 +174,18 @@ typedef struct {
 int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* offsets, const int32_t* max_new,
                  int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats,
                  double* out_times);
+/* The scheduler of tsl_generate with no model and no device: the same
+ * admission, page allocation and step inputs, where each step's next token
+ * for request r is taken in order from script (laid out as out_tokens), so
+ * the integer stream sched.rs feeds Engine::step (src/llm/sched.rs:52-179:
+ * slots :98 and :141, LIFO pages :60 :88 :125 :168) can be checked on a CPU.
+ * Every step appends to trace: mode, n, nwant, tokens[n], pos[n], slots[n],
+ * starts[n] (mode 1 only), tables[n * max_seq_pages] and lens[n] (mode 2
+ * only), want[nwant]. *used receives the words written (or needed, when
+ * more than cap). Errors as tsl_generate. */
+int tsl_schedule_trace(const tsl_limits* lim, int eos, int nreq, const int32_t* prompts, const int64_t* offsets,
+                       const int32_t* max_new, int max_batch, int packed, const int32_t* script, int32_t* out_tokens,
+                       int32_t* out_counts, tsl_stats* stats, int32_t* trace, int64_t cap, int64_t* used);
 
 /* ---- checkpoints (src/llm/safetensors.rs) */
 

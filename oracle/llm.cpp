@@ -109,6 +109,8 @@ int tsl_ref_forward(const Cfg* cfg, const u16* embed, const u16* layers, const u
     auto matvec = [](const std::vector<float>& w, const std::vector<float>& x, i64 rows) {
         i64 cols = (i64)x.size();
         std::vector<float> y(rows);
+        // Rows in parallel; each row's sum stays the sequential f32 loop.
+#pragma omp parallel for schedule(static) if (rows * cols > (1 << 20))
         for (i64 r = 0; r < rows; r++) {
             float s = 0.0f;
             for (i64 k = 0; k < cols; k++) s += w[r * cols + k] * x[k];

@@ -48,7 +48,7 @@ EXPORTS = [
     "tsl_event_elapsed", "tsl_weights_sizes", "tsl_weights_random", "tsl_engine_new", "tsl_engine_free",
     "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
     "tsl_checkpoint_save", "tsl_json_roundtrip", "tsl_rng_new", "tsl_rng_bits", "tsl_rng_tensor",
-    "tsl_time_each", "tsl_engine_profile", "tsl_engine_profile_rows",
+    "tsl_time_each", "tsl_engine_profile", "tsl_engine_profile_rows", "tsl_schedule_trace",
 ]
 
 
@@ -113,6 +113,8 @@ def _declare(L):
     L.tsl_engine_set.argtypes = [_INT, _INT, _INT]
     L.tsl_engine_step.argtypes = [_INT, _INT, _P, _P, _P, _INT, _P, _INT, _P, _P, _INT, _P, _P]
     L.tsl_generate.argtypes = [_INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, ctypes.POINTER(Stats), _P]
+    L.tsl_schedule_trace.argtypes = [ctypes.POINTER(Limits), _INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, _P,
+                                     ctypes.POINTER(Stats), _P, _I64, ctypes.POINTER(_I64)]
     L.tsl_checkpoint_config.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config)]
     L.tsl_checkpoint_load.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config), _P, _P, _P, _P, ctypes.POINTER(_INT)]
     L.tsl_checkpoint_save.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config), _P, _P, _P, _P]
@@ -479,6 +481,63 @@ class Engine:
             res.append(out[base:base + counts[i]].tolist())
             base += int(m)
         return res, st
+
+
+def schedule_trace(limits, eos, requests, max_batch, packed, script):
+    """The scheduler of Engine.generate run on the CPU with no model
+    (tsl_schedule_trace): requests = [(prompt tokens, max_new)], script =
+    per request the token ids its steps return, in order. Returns (the steps
+    as dicts of the integer inputs sched.rs hands Engine::step, token lists,
+    Stats)."""
+    prompts = _i32([t for p, _ in requests for t in p])
+    offsets = np.zeros(len(requests) + 1, np.int64)
+    offsets[1:] = np.cumsum([len(p) for p, _ in requests])
+    max_new = _i32([m for _, m in requests])
+    flat = np.zeros(max(int(max_new.clip(0).sum()), 1), np.int32)
+    base = 0
+    for (_, m), sc in zip(requests, script):
+        flat[base:base + min(len(sc), max(m, 0))] = sc[:max(m, 0)]
+        base += max(m, 0)
+    out = np.zeros_like(flat)
+    counts = np.zeros(max(len(requests), 1), np.int32)
+    st = Stats()
+    used = _I64(0)
+    cap = 1 << 16
+    while True:
+        trace = np.zeros(cap, np.int32)
+        r = lib().tsl_schedule_trace(ctypes.byref(limits), int(eos), len(requests), prompts.ctypes.data,
+                                     offsets.ctypes.data, max_new.ctypes.data, int(max_batch), int(packed),
+                                     flat.ctypes.data, out.ctypes.data, counts.ctypes.data, ctypes.byref(st),
+                                     trace.ctypes.data, cap, ctypes.byref(used))
+        if r != 0 and used.value > cap:
+            cap = int(used.value)
+            continue
+        check(r)
+        break
+    steps, i, mp = [], 0, limits.max_seq_pages
+    while i < used.value:
+        mode, n, nw = (int(x) for x in trace[i:i + 3])
+        i += 3
+        s = {"mode": mode}
+        for k in ("tokens", "pos", "slots"):
+            s[k] = trace[i:i + n].tolist()
+            i += n
+        if mode == 1:
+            s["starts"] = trace[i:i + n].tolist()
+            i += n
+        if mode == 2:
+            s["tables"] = trace[i:i + n * mp].reshape(n, mp).tolist()
+            i += n * mp
+            s["lens"] = trace[i:i + n].tolist()
+            i += n
+        s["want"] = trace[i:i + nw].tolist()
+        i += nw
+        steps.append(s)
+    toks, base = [], 0
+    for k, (_, m) in enumerate(requests):
+        toks.append(out[base:base + counts[k]].tolist())
+        base += m
+    return steps, toks, st
 
 
 class Rng:

@@ -19,7 +19,7 @@ ARCH = "gfx950"
 # otherwise form them from plain float code.
 HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall"]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-mf16c"]  # f16 conversions in hardware
 
 SOURCES = ["runtime.hip", "gemm.hip", "attention.hip", "decode.hip", "rows.hip"]
 HOST_SOURCES = ["engine.cpp", "checkpoint.cpp"]

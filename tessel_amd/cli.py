@@ -327,6 +327,8 @@ def llm(args):
     if not isinstance(ps, list):
         raise CliError(f"{path}: not a JSON list")
     max_new = num("--max-new", 64)
+    if max_new < 1:
+        raise CliError("--max-new must be at least 1")
     reqs = []
     for p in ps:
         if not isinstance(p, list):

@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
     const half2v ones = {(half_t)1.0f, (half_t)1.0f};
 
     const int kend = min(q0 + BQW, a.S);
-    const int kbeg = PREFILL ? (a.starts[q0] / BKEY) * BKEY : 0;
+    const int kbeg = PREFILL ? (max(a.starts[q0], 0) / BKEY) * BKEY : 0;  // a negative start reads no memory before K/V
     const int nblk = kbeg < kend ? (kend - kbeg + BKEY - 1) / BKEY : 0;
     const int nit = (nblk + KS - 1) / KS;
     if (nit > 0) issue(0, 0, kbeg, nblk);

@@ -1104,25 +1104,33 @@ int nchunks(const TslKernel& k) {
 
 }  // namespace
 
-// Sizes the per-chunk partial buffer once, when the kernel is specialised.
-int prepare_decode(TslKernel& k) {
+// Checks a decode specialisation and gives the scratch bytes its launch
+// needs (0: none): the stream path's range states then its [B + 1] unit
+// prefix, or the chunked path's [B][G][NCH][QPG][2 + D] per-chunk states.
+static int decode_scratch_bytes(const TslKernel& k, size_t* bytes) {
     int64_t D = k.dim("D"), H = k.dim("H");
     int64_t G = k.name == "paged_attention" ? H : k.dim("G");
+    *bytes = 0;
     if (D != 16 && D != 32 && D != 64 && D != 128)
         return tsl_fail(-2, k.name + ": head dimension " + std::to_string(D) + " unsupported (16, 32, 64 or 128)");
     if (G <= 0 || H % G != 0) return tsl_fail(-2, k.name + ": H must be a multiple of G");
     int64_t qpg = H / G;
     if (qpg != 1 && qpg != 2 && qpg != 4 && qpg != 8 && qpg != 16)
         return tsl_fail(-2, k.name + ": H / G must be 1, 2, 4, 8 or 16");
-    if (stream_path(k)) {  // range states, then the [B + 1] unit prefix
-        size_t bytes = stream_state_bytes(k) + (size_t)(k.dim("B") * (G / stream_nwv(G)) + 1) * 4;
-        if (tsl_hip_check(hipMalloc(&k.scratch, bytes), "decode_attention scratch")) return -1;
-        k.scratch_bytes = bytes;
+    if (stream_path(k)) {
+        *bytes = stream_state_bytes(k) + (size_t)(k.dim("B") * (G / stream_nwv(G)) + 1) * 4;
         return 0;
     }
     int nch = nchunks(k);
-    if (nch > 1) {  // [B][G][NCH][QPG][2 + D] per-chunk states
-        size_t bytes = (size_t)k.dim("B") * G * nch * qpg * (2 + D) * sizeof(float);
+    if (nch > 1) *bytes = (size_t)k.dim("B") * G * nch * qpg * (2 + D) * sizeof(float);
+    return 0;
+}
+
+// Sizes the partial-state buffer once, when the kernel is specialised.
+int prepare_decode(TslKernel& k) {
+    size_t bytes = 0;
+    if (int r = decode_scratch_bytes(k, &bytes)) return r;
+    if (bytes) {
         if (tsl_hip_check(hipMalloc(&k.scratch, bytes), "decode_attention scratch")) return -1;
         k.scratch_bytes = bytes;
     }

@@ -393,6 +393,11 @@ struct Engine {
         size_t bw = nwant ? padded(nwant) : 0;
         if (mode != PREFILL && mode != PACKED && mode != DECODE) return tsl_fail(TSL_ERR_ARG, "unknown attention mode");
         if (mode == PACKED && !st_in) return tsl_fail(TSL_ERR_ARG, "packed prefill: one start per token");
+        if (mode == PACKED)  // each row's sequence starts at or before it, and sequences do not overlap
+            for (size_t i = 0; i < n; i++)
+                if (st_in[i] < 0 || (size_t)st_in[i] > i || (i > 0 && st_in[i] < st_in[i - 1]))
+                    return tsl_fail(TSL_ERR_ARG, "packed prefill: starts must satisfy 0 <= starts[i] <= i, "
+                                                 "non-decreasing");
         if (mode == DECODE && nseq > t) return tsl_fail(TSL_ERR_ARG, "decode: more sequences than rows");
         if (bw > t) return tsl_fail(TSL_ERR_ARG, "more logits rows than step rows");
         // Every input of the step in the arena's layout for t, one upload.
@@ -605,19 +610,65 @@ int tsl_engine_step(int engine, int n, const int32_t* tokens, const int32_t* pos
                    logits);
 }
 
-// sched::generate_with (src/llm/sched.rs:52-179).
-int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* offsets, const int32_t* max_new,
-                 int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats,
-                 double* out_times) {
-    Engine* e = get(engine);
-    if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
+}  // extern "C"
+
+namespace {
+
+// One step of the scheduler's model, as sched.rs calls Engine::step: the
+// rows' tokens, positions and cache slots, the attention mode with its
+// starts (packed prefill) or tables and lens (decode), and the rows whose
+// next token is wanted; `ids` names the request each wanted row belongs
+// to. Writes one token id per wanted row into `next`.
+struct StepIn {
+    int mode;
+    const std::vector<int32_t>& toks;
+    const std::vector<int32_t>& pos;
+    const std::vector<int32_t>& slots;
+    const std::vector<int32_t>& starts;
+    size_t nseq;
+    const std::vector<int32_t>& tables;
+    const std::vector<int32_t>& lens;
+    const std::vector<int32_t>& want;
+    const std::vector<int>& ids;
+};
+
+struct Sched {
+    tsl_limits lim;
+    int eos;
+};
+
+// sched::generate_with (src/llm/sched.rs:52-179): admission by token
+// budget, batch size and free pages (whole sequences reserved up front),
+// the LIFO page free list, one packed (or single) prefill step for what
+// was admitted, else one decode step for every running sequence.
+// Requests are validated before anything runs: an empty or too long
+// prompt, max_new < 1, or more pages than a sequence (or the pool) can
+// hold is an error (the reference panics on max_new = 0 and waits for
+// ever on a request larger than the pool).
+template <class Step>
+int schedule(const Sched& sc, int nreq, const int32_t* prompts, const int64_t* offsets, const int32_t* max_new,
+             int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats,
+             double* out_times, Step&& step) {
     using clk = std::chrono::steady_clock;
     auto start = clk::now();
-    const int p = e->lim.page;
-    const int vocab = e->cfg.vocab;
-    const size_t mp = e->lim.max_seq_pages;
+    const int p = sc.lim.page;
+    const size_t mp = sc.lim.max_seq_pages;
+    if (nreq < 0 || max_batch < 1 || p < 1) return tsl_fail(TSL_ERR_ARG, "generate: bad request count or batch");
+    for (int id = 0; id < nreq; id++) {
+        int64_t plen = offsets[id + 1] - offsets[id];
+        std::ostringstream m;
+        if (max_new[id] < 1) {
+            m << "request " << id << ": max_new must be at least 1";
+            return tsl_fail(TSL_ERR_ARG, m.str());
+        }
+        size_t need = plen > 0 ? ((size_t)plen + (size_t)max_new[id] + p - 1) / p : 0;
+        if (plen <= 0 || plen > sc.lim.max_tokens || need > mp || need > (size_t)sc.lim.pages) {
+            m << "request " << id << ": prompt of " << plen << " tokens does not fit";
+            return tsl_fail(TSL_ERR_ARG, m.str());
+        }
+    }
     std::vector<int32_t> free_pages;
-    for (int i = e->lim.pages - 1; i >= 0; i--) free_pages.push_back(i);
+    for (int i = sc.lim.pages - 1; i >= 0; i--) free_pages.push_back(i);
     std::deque<int> waiting;
     for (int i = 0; i < nreq; i++) waiting.push_back(i);
     struct Seq {
@@ -632,8 +683,7 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
     for (int i = 1; i < nreq; i++) out_base[i] = out_base[i - 1] + max_new[i - 1];
     for (int i = 0; i < nreq; i++) out_counts[i] = 0;
     tsl_stats st{};
-    max_batch = std::min(max_batch, e->lim.max_tokens);
-    const int eos = e->cfg.eos;
+    max_batch = std::min(max_batch, sc.lim.max_tokens);
     auto since = [&]() { return std::chrono::duration<double>(clk::now() - start).count(); };
     if (out_times)
         for (int i = 0; i < 2 * nreq; i++) out_times[i] = 0.0;
@@ -644,6 +694,7 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
     auto done = [&](int id) {
         if (out_times) out_times[2 * id + 1] = since();  // done_s
     };
+    const std::vector<int32_t> none;
     while (!waiting.empty() || !running.empty()) {
         std::vector<std::pair<int, std::vector<int32_t>>> admit;
         size_t tokens = 0;
@@ -651,12 +702,7 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
             int id = waiting.front();
             size_t plen = (size_t)(offsets[id + 1] - offsets[id]);
             size_t need = (plen + max_new[id] + p - 1) / p;
-            if (plen == 0 || plen > (size_t)e->lim.max_tokens || need > mp) {
-                std::ostringstream m;
-                m << "request " << id << ": prompt of " << plen << " tokens does not fit";
-                return tsl_fail(TSL_ERR_ARG, m.str());
-            }
-            bool room = (int)(running.size() + admit.size()) < max_batch && tokens + plen <= (size_t)e->lim.max_tokens;
+            bool room = (int)(running.size() + admit.size()) < max_batch && tokens + plen <= (size_t)sc.lim.max_tokens;
             if (!room || need > free_pages.size() || (!packed && !admit.empty())) break;
             waiting.pop_front();
             tokens += plen;
@@ -669,6 +715,7 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
         }
         if (!admit.empty()) {
             std::vector<int32_t> toks, pos, slots, starts, last;
+            std::vector<int> ids;
             for (auto& a : admit) {
                 const int32_t* pr = prompts + offsets[a.first];
                 size_t plen = (size_t)(offsets[a.first + 1] - offsets[a.first]);
@@ -680,13 +727,11 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
                     starts.push_back(s0);
                 }
                 last.push_back((int32_t)toks.size() - 1);
+                ids.push_back(a.first);
             }
-            // The next tokens come from the GPU's argmax (fused/argmax, the
-            // same first-largest rule as argmax here), not from the logits.
             std::vector<int32_t> next(last.size());
             int mode = admit.size() == 1 ? PREFILL : PACKED;
-            TRY(e->step(toks.size(), toks.data(), pos.data(), slots.data(), mode, starts.data(), 0, nullptr, nullptr,
-                        last.size(), last.data(), nullptr, next.data()));
+            TRY(step(StepIn{mode, toks, pos, slots, starts, 0, none, none, last, ids}, next.data()));
             st.prefill_steps++;
             st.prompt_tokens += toks.size();
             for (size_t i = 0; i < admit.size(); i++) {
@@ -695,7 +740,7 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
                 emit(id, t);
                 size_t plen = (size_t)(offsets[id + 1] - offsets[id]);
                 Seq s{id, admit[i].second, plen, t, max_new[id] - 1};
-                if (s.left == 0 || t == eos) {
+                if (s.left == 0 || t == sc.eos) {
                     done(id);
                     free_pages.insert(free_pages.end(), s.pages.begin(), s.pages.end());
                 } else {
@@ -704,10 +749,11 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
             }
             continue;
         }
-        if (running.empty()) continue;
+        if (running.empty()) continue;  // unreachable: every request fits the empty pool
         auto t0 = clk::now();
         size_t nb = running.size();
         std::vector<int32_t> toks, pos, slots, tables(nb * mp, 0), lens, want;
+        std::vector<int> ids;
         for (size_t b = 0; b < nb; b++) {
             const Seq& s = running[b];
             toks.push_back(s.last);
@@ -716,10 +762,10 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
             std::copy(s.pages.begin(), s.pages.end(), tables.begin() + b * mp);
             lens.push_back((int32_t)s.len + 1);
             want.push_back((int32_t)b);
+            ids.push_back(s.id);
         }
         std::vector<int32_t> next(nb);
-        TRY(e->step(nb, toks.data(), pos.data(), slots.data(), DECODE, nullptr, nb, tables.data(), lens.data(), nb,
-                    want.data(), nullptr, next.data()));
+        TRY(step(StepIn{DECODE, toks, pos, slots, none, nb, tables, lens, want, ids}, next.data()));
         st.decode_steps++;
         st.largest_batch = std::max<int64_t>(st.largest_batch, nb);
         st.decode_tokens += nb;
@@ -731,7 +777,7 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
             s.last = t;
             s.left--;
             emit(s.id, t);
-            if (s.left == 0 || t == eos) {
+            if (s.left == 0 || t == sc.eos) {
                 done(s.id);
                 free_pages.insert(free_pages.end(), s.pages.begin(), s.pages.end());
             } else {
@@ -745,6 +791,63 @@ int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* of
     st.seconds = std::chrono::duration<double>(clk::now() - start).count();
     if (stats) *stats = st;
     return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsl_generate(int engine, int nreq, const int32_t* prompts, const int64_t* offsets, const int32_t* max_new,
+                 int max_batch, int packed, int32_t* out_tokens, int32_t* out_counts, tsl_stats* stats,
+                 double* out_times) {
+    Engine* e = get(engine);
+    if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
+    // The next tokens come from the GPU's argmax (fused/argmax, the same
+    // first-largest rule as src/llm/mod.rs:132-140), not from the logits.
+    auto step = [&](const StepIn& s, int32_t* next) {
+        return e->step(s.toks.size(), s.toks.data(), s.pos.data(), s.slots.data(), s.mode,
+                       s.mode == PACKED ? s.starts.data() : nullptr, s.nseq, s.tables.data(), s.lens.data(),
+                       s.want.size(), s.want.data(), nullptr, next);
+    };
+    return schedule(Sched{e->lim, e->cfg.eos}, nreq, prompts, offsets, max_new, max_batch, packed, out_tokens,
+                    out_counts, stats, out_times, step);
+}
+
+int tsl_schedule_trace(const tsl_limits* lim, int eos, int nreq, const int32_t* prompts, const int64_t* offsets,
+                       const int32_t* max_new, int max_batch, int packed, const int32_t* script, int32_t* out_tokens,
+                       int32_t* out_counts, tsl_stats* stats, int32_t* trace, int64_t cap, int64_t* used) {
+    if (!lim || !trace || !used || cap < 0) return tsl_fail(TSL_ERR_ARG, "schedule trace: null argument");
+    std::vector<size_t> base(nreq > 0 ? nreq : 0, 0);
+    for (int i = 1; i < nreq; i++) base[i] = base[i - 1] + (max_new[i - 1] > 0 ? max_new[i - 1] : 0);
+    std::vector<int> emitted(base.size(), 0);
+    int64_t w = 0;
+    auto put = [&](const int32_t* v, size_t n) {
+        if (w + (int64_t)n <= cap) std::copy(v, v + n, trace + w);
+        w += (int64_t)n;
+    };
+    auto step = [&](const StepIn& s, int32_t* next) {
+        const int32_t head[3] = {s.mode, (int32_t)s.toks.size(), (int32_t)s.want.size()};
+        put(head, 3);
+        put(s.toks.data(), s.toks.size());
+        put(s.pos.data(), s.pos.size());
+        put(s.slots.data(), s.slots.size());
+        if (s.mode == PACKED) put(s.starts.data(), s.starts.size());
+        if (s.mode == DECODE) {
+            put(s.tables.data(), s.tables.size());
+            put(s.lens.data(), s.lens.size());
+        }
+        put(s.want.data(), s.want.size());
+        for (size_t i = 0; i < s.want.size(); i++) {
+            int id = s.ids[i];
+            next[i] = script[base[id] + emitted[id]++];
+        }
+        return 0;
+    };
+    int r = schedule(Sched{*lim, eos}, nreq, prompts, offsets, max_new, max_batch, packed, out_tokens, out_counts,
+                     stats, nullptr, step);
+    *used = w;
+    if (r == 0 && w > cap) return tsl_fail(TSL_ERR_ARG, "schedule trace: buffer too small");
+    return r;
 }
 
 }  // extern "C"

@@ -151,3 +151,98 @@ def test_close_then_launch():
     a = np.ones((64, 64), np.float16)
     c = T.run("matmul", "matmul", [a, a, np.zeros((64, 64), np.float16)], outputs=[2])[2]
     assert (c == 64).all()
+
+
+def _tinyllama_engine(seqs=32, prompt=512, new=128, graphs=True):
+    # BASELINE config 5's engine: TinyLlama-1.1B shape, Weights::random(7)
+    # (the library's generator, equal to the oracle's bit for bit:
+    # tests/test_abi.py), page 16, 1024-token steps.
+    cfg = T.Config.tinyllama()
+    w = T.weights_random(cfg, 7)
+    mp = (prompt + new + 15) // 16
+    e = T.Engine(cfg, T.Limits(16, seqs * mp + 64, 1024, mp), w, graphs=graphs)
+    return cfg, w, e
+
+
+def test_tinyllama_shape_against_the_reference(gpu):
+    """Config 5's model (22 layers, 32/4 heads, D 64, FFN 5632, vocab 32000)
+    against reference::forward (src/llm/reference.rs): prefill logits of a
+    24-token prompt at three rows, then a batched greedy generation whose
+    every token is the reference's argmax or within 2e-2 of its scale
+    (tests/llm.rs:26-82)."""
+    cfg, w, e = _tinyllama_engine(seqs=2, prompt=32, new=8)
+    ocfg = oracle.Config.tinyllama()
+    rng = np.random.default_rng(3)
+    p1 = rng.integers(3, cfg.vocab, 24).tolist()
+    p2 = rng.integers(3, cfg.vocab, 17).tolist()
+    n = len(p1)
+    got = e.step(p1, list(range(n)), list(range(n)), T.Engine.PREFILL, want=[0, 11, n - 1])
+    reqs = [(p1, 8), (p2, 6)]
+    outs, st = e.generate(reqs, 2)
+    e.close()
+    assert st.largest_batch == 2 and [len(o) for o in outs] == [8, 6]
+    exact = total = 0
+    for k, ((p, m), toks) in enumerate(zip(reqs, outs)):
+        seq = list(p) + toks[:-1]
+        ref = oracle.forward(ocfg, w, seq)  # logits after every position of the history
+        if k == 0:
+            for row, r in zip(got, (0, 11, n - 1)):
+                err = rel(row, ref[r])
+                print(f"tinyllama prefill row {r}: logits within {err:.2e} of the reference", flush=True)
+                assert err < 2e-2
+        for i, t in enumerate(toks):
+            l = ref[len(p) - 1 + i]
+            best = oracle.argmax(l)
+            scale = np.abs(l).max()
+            assert t == best or l[best] - l[t] < 2e-2 * scale, (k, i, t, best)
+            exact += t == best
+            total += 1
+    print(f"tinyllama generation: {exact} of {total} tokens the reference's own choice", flush=True)
+
+
+def test_tinyllama_full_config_properties(gpu):
+    """Config 5 at full size (32 prompts of 512 random ids, 128 greedy
+    steps): packed prefill (two prompts per 1024-token step) and one prompt
+    per step generate the same token streams, graph replay equals eager
+    launches, every request gets 128 tokens (or stops at eos), and the
+    statistics count what ran."""
+    cfg, w, e = _tinyllama_engine()
+    del w
+    rng = np.random.default_rng(5)
+    reqs = [(rng.integers(3, cfg.vocab, 512).tolist(), 128) for _ in range(32)]
+    packed, st = e.generate(reqs, 32)
+    print(f"config 5: {st.generated} tokens, {st.prefill_steps} prefill + {st.decode_steps} decode steps", flush=True)
+    assert st.prefill_steps == 16 and st.prompt_tokens == 32 * 512 and st.largest_batch == 32
+    assert st.generated == sum(len(o) for o in packed)
+    assert st.decode_tokens == st.generated - 32
+    for o in packed:
+        assert len(o) == 128 or (len(o) < 128 and o[-1] == cfg.eos and cfg.eos not in o[:-1])
+    e.set(False, True)
+    eager, _ = e.generate(reqs, 32)
+    assert eager == packed
+    e.set(True, True)
+    single, st1 = e.generate(reqs, 32, packed=False)
+    assert st1.prefill_steps == 32
+    e.close()
+    same = sum(a == b for a, b in zip(single, packed))
+    print(f"config 5: one prompt per step == packed for {same} of 32 requests", flush=True)
+    assert single == packed
+
+
+def test_engine_rejects_bad_requests_and_starts(gpu):
+    # max_new 0 and a request larger than the page pool are refused before
+    # any step runs; packed starts must satisfy 0 <= starts[i] <= i and be
+    # non-decreasing (a start outside the rows would address K/V before or
+    # past the step).
+    cfg = T.Config.tiny()
+    e = T.Engine(cfg, limits(), T.weights_random(cfg, 3))
+    with pytest.raises(RuntimeError, match="max_new must be at least 1"):
+        e.generate([([1, 2, 3], 2), ([4, 5], 0)], 2)
+    with pytest.raises(RuntimeError, match="does not fit"):
+        T.Engine.generate(e, [([1] * 16, 300)], 1)
+    for bad in ([0, 0, -1, 3], [0, 0, 3, 3], [0, 1, 0, 3]):
+        with pytest.raises(RuntimeError, match="starts"):
+            e.step([1, 2, 3, 4], [0, 1, 0, 1], [0, 1, 2, 3], T.Engine.PACKED, starts=bad, want=[3])
+    got = e.step([1, 2, 3, 4], [0, 1, 0, 1], [0, 1, 2, 3], T.Engine.PACKED, starts=[0, 0, 2, 2], want=[1, 3])
+    assert np.isfinite(got).all()
+    e.close()

@@ -241,6 +241,22 @@ def test_flash_attention_long_sampled(s):
         parity(f"flash row {hh},{i}", got[hh, i], want)
 
 
+@pytest.mark.parametrize("s", [2048, 4096])
+def test_flash_attention_long_whole_heads_vs_oracle(s):
+    # BASELINE config 3 at its long sizes: the 32-head launch, with four
+    # whole heads (every row) against the interpreter restatement of
+    # kernels/attention.tl:4-24 (heads are independent programs, so the
+    # oracle runs on just those heads' slices).
+    _say("flash long heads", s)
+    rng = np.random.default_rng(s + 1)
+    q, k, v = (rng.standard_normal((32, s, 64)).astype(np.float16) for _ in range(3))
+    got = T.run("attention", "flash_attention", [q, k, v, np.zeros_like(q)], [T.F32(0.125)], outputs=[3])[3]
+    heads = [0, 9, 22, 31]
+    sl = lambda x: np.ascontiguousarray(x[heads])
+    want = oracle.flash_attention(sl(q), sl(k), sl(v), 0.125, threads=16)
+    parity(f"flash S={s} heads {heads}", got[heads], want)
+
+
 def _packed(seed, lens, h, g, d):
     r = oracle.Rng(seed)
     s = sum(lens)
@@ -337,9 +353,9 @@ def test_decode_attention_vs_oracle(cfg):
 
 
 def test_decode_attention_repeat_launches():
-    """Multi-chunk sequences merge through per-(b, g) arrival counts that the
-    kernel returns to zero: back-to-back launches on one handle agree bit for
-    bit, and with the oracle."""
+    """Multi-chunk sequences write per-chunk partial states into the handle's
+    scratch and a second kernel merges them: back-to-back launches on one
+    handle (reusing that scratch) agree bit for bit, and with the oracle."""
     _say("decode repeat")
     q, kc, vc, table, lens, scale = decode_case(4, b=12, h=32, g=8, d=128, p=16, lo=300, hi=4096)
     T.open()
