@@ -101,6 +101,26 @@ int tsl_replay(int graph);
 int tsl_event_record(int* event);
 int tsl_event_elapsed(int start, int end, float* ms);
 
+/*
+ * decode_attention (kernels/llm.tl:150-172) with no allocation. This entry
+ * point has no counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). It takes the arguments of the
+ * decode_attention launch as plain device pointers and sizes (q [B,H,D],
+ * kc/vc [NP,P,G,D] f16; table i32 [B,MP]; lens i32 [B]; o [B,H,D] f16),
+ * runs the same kernels as tsl_launch of a decode_attention handle, and
+ * keeps their partial states in a library-owned device array of
+ * TSL_NOALLOC_SCRATCH_BYTES per GPU (resident until the process ends)
+ * instead of a per-handle allocation. A shape needing more scratch is
+ * TSL_ERR_ARG. Every call on one GPU shares that array: calls that overlap
+ * on one GPU (other threads, other streams) race. Nothing in it needs to
+ * start at zero; the kernels write every state they read. Asynchronous on
+ * the library stream; calls no hipMalloc/hipFree.
+ */
+#define TSL_NOALLOC_SCRATCH_BYTES (64u << 20)
+int tsl_decode_attention_noalloc(uint64_t q, uint64_t kc, uint64_t vc, uint64_t table, uint64_t lens, uint64_t o,
+                                 float scale, int B, int H, int G, int D, int NP, int P, int MP);
+
 /* ---- the LLM engine (src/llm/engine.rs, src/llm/sched.rs, src/llm/mod.rs) */
 
 /* Config (src/llm/mod.rs:15-28). */

@@ -49,6 +49,7 @@ EXPORTS = [
     "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
     "tsl_checkpoint_save", "tsl_json_roundtrip", "tsl_rng_new", "tsl_rng_bits", "tsl_rng_tensor",
     "tsl_time_each", "tsl_engine_profile", "tsl_engine_profile_rows", "tsl_schedule_trace",
+    "tsl_decode_attention_noalloc",
 ]
 
 
@@ -113,6 +114,7 @@ def _declare(L):
     L.tsl_engine_set.argtypes = [_INT, _INT, _INT]
     L.tsl_engine_step.argtypes = [_INT, _INT, _P, _P, _P, _INT, _P, _INT, _P, _P, _INT, _P, _P]
     L.tsl_generate.argtypes = [_INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, ctypes.POINTER(Stats), _P]
+    L.tsl_decode_attention_noalloc.argtypes = [_U64] * 6 + [ctypes.c_float] + [_INT] * 7
     L.tsl_schedule_trace.argtypes = [ctypes.POINTER(Limits), _INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, _P,
                                      ctypes.POINTER(Stats), _P, _I64, ctypes.POINTER(_I64)]
     L.tsl_checkpoint_config.argtypes = [ctypes.c_char_p, ctypes.POINTER(Config)]

@@ -18,6 +18,10 @@
 // lens[b] == 0 gives 0/0 = NaN, as in the .tl.
 #include "common.h"
 
+#include <mutex>
+
+#include "../../include/tessel.h"
+
 #include <algorithm>
 
 namespace {
@@ -1178,4 +1182,59 @@ int launch_decode_attention(TslKernel& k, const uint64_t* args, hipStream_t s) {
 
 int launch_paged_attention(TslKernel& k, const uint64_t* args, hipStream_t s) {
     return launch_decode_common(k, args, s, false);
+}
+
+// ---------------------------------------------------------------- no-alloc entry
+
+// The scratch of tsl_decode_attention_noalloc: one array per GPU, resident
+// until the process ends, shared by every call on that GPU. Host code uses
+// only the address hipGetSymbolAddress gives for the current device, never
+// the array's name (a host-side stand-in, not a device address).
+static __device__ __align__(256) char scratch[TSL_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[NOALLOC_MAX_DEVICES];
+
+// The current device's scratch address, looked up once per device.
+int noalloc_scratch(void** out) {
+    int dev = 0;
+    if (tsl_hip_check(hipGetDevice(&dev), "hipGetDevice")) return -1;
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return tsl_fail(-2, "decode_attention_noalloc: device index too large");
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* p = nullptr;
+        if (tsl_hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return -1;
+        g_noalloc_ptr[dev] = p;
+    }
+    *out = g_noalloc_ptr[dev];
+    return 0;
+}
+}  // namespace
+
+extern "C" int tsl_decode_attention_noalloc(uint64_t q, uint64_t kc, uint64_t vc, uint64_t table, uint64_t lens,
+                                            uint64_t o, float scale, int B, int H, int G, int D, int NP, int P,
+                                            int MP) {
+    if (B < 0 || H <= 0 || G <= 0 || D <= 0 || NP <= 0 || P <= 0 || MP <= 0 || (P & (P - 1)))
+        return tsl_fail(-2, "decode_attention_noalloc: sizes must be positive (B >= 0) and P a power of two");
+    if (tsl_open()) return -1;
+    TslKernel k;
+    k.file = "llm";
+    k.name = "decode_attention";
+    k.nparams = 7;
+    k.dims = {{"B", B}, {"H", H}, {"D", D}, {"NP", NP}, {"P", P}, {"G", G}, {"MP", MP}};
+    size_t bytes = 0;
+    if (int r = decode_scratch_bytes(k, &bytes)) return r;
+    if (bytes > sizeof(scratch))
+        return tsl_fail(-2, "decode_attention_noalloc: this shape needs " + std::to_string(bytes) +
+                                " bytes of scratch; at most " + std::to_string(sizeof(scratch)));
+    void* ptr = nullptr;
+    if (int r = noalloc_scratch(&ptr)) return r;
+    k.scratch = ptr;
+    k.scratch_bytes = sizeof(scratch);
+    uint32_t sb;
+    __builtin_memcpy(&sb, &scale, 4);
+    const uint64_t args[7] = {q, kc, vc, table, lens, o, (uint64_t)sb};
+    return launch_decode_common(k, args, (hipStream_t)tsl_stream(), true);
 }
