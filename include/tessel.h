@@ -95,6 +95,11 @@ int tsl_time_each(int handle, const uint64_t* args, int nargs, int iters, float*
 int tsl_capture_begin(void);
 /* Ends the recording and instantiates it: *graph identifies it. */
 int tsl_capture_end(int* graph);
+/* The nodes a recorded graph holds, counted by type when it was recorded
+ * (hipGraphGetNodes before instantiation): counts[0] kernels, [1] memsets,
+ * [2] memcpys, [3] any other node. No reference counterpart: a check that
+ * captured sequences are kernels only. */
+int tsl_graph_nodes(int graph, int64_t* counts);
 /* Replays a recorded graph asynchronously (src/driver.rs:360-363). */
 int tsl_replay(int graph);
 /* Events on the stream, for timing a caller's own sequence. */
@@ -168,6 +173,11 @@ int tsl_engine_set(int engine, int graphs, int tune);
  * the text (NUL-terminated) when cap > *len. */
 int tsl_engine_profile(int engine, int on);
 int tsl_engine_profile_rows(int engine, char* out, size_t cap, size_t* len);
+
+/* The decode-step graphs the engine has recorded (src/llm/engine.rs:
+ * 330-350 keeps one per padded batch size): up to cap (rows, graph) pairs
+ * into rows/graphs, *n the number recorded. */
+int tsl_engine_graphs(int engine, int32_t* rows, int32_t* graphs, int cap, int* n);
 
 /* Engine::step (src/llm/engine.rs:275-354). mode 0 = Prefill, 1 = Packed
  * (starts[n]), 2 = Decode (tables: nseq rows of max_seq_pages pages, lens:

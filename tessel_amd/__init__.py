@@ -49,6 +49,7 @@ EXPORTS = [
     "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
     "tsl_checkpoint_save", "tsl_json_roundtrip", "tsl_rng_new", "tsl_rng_bits", "tsl_rng_tensor",
     "tsl_time_each", "tsl_engine_profile", "tsl_engine_profile_rows", "tsl_schedule_trace",
+    "tsl_graph_nodes", "tsl_engine_graphs",
     "tsl_decode_attention_noalloc",
 ]
 
@@ -114,6 +115,8 @@ def _declare(L):
     L.tsl_engine_set.argtypes = [_INT, _INT, _INT]
     L.tsl_engine_step.argtypes = [_INT, _INT, _P, _P, _P, _INT, _P, _INT, _P, _P, _INT, _P, _P]
     L.tsl_generate.argtypes = [_INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, ctypes.POINTER(Stats), _P]
+    L.tsl_graph_nodes.argtypes = [_INT, _P]
+    L.tsl_engine_graphs.argtypes = [_INT, _P, _P, _INT, ctypes.POINTER(_INT)]
     L.tsl_decode_attention_noalloc.argtypes = [_U64] * 6 + [ctypes.c_float] + [_INT] * 7
     L.tsl_schedule_trace.argtypes = [ctypes.POINTER(Limits), _INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, _P,
                                      ctypes.POINTER(Stats), _P, _I64, ctypes.POINTER(_I64)]
@@ -305,6 +308,13 @@ def replay(g):
     check(lib().tsl_replay(int(g)))
 
 
+def graph_nodes(g):
+    """Node counts of recorded graph g by type: kernel, memset, memcpy, other."""
+    c = np.zeros(4, np.int64)
+    check(lib().tsl_graph_nodes(int(g), c.ctypes.data))
+    return dict(zip(("kernel", "memset", "memcpy", "other"), c.tolist()))
+
+
 def event_record():
     e = _INT()
     check(lib().tsl_event_record(ctypes.byref(e)))
@@ -448,6 +458,12 @@ class Engine:
                                     ln.ctypes.data if ln is not None else None, want.size,
                                     want.ctypes.data if want.size else None, out.ctypes.data))
         return out
+
+    def graphs(self):
+        """{padded rows: graph} of the decode steps recorded so far."""
+        rows, ids, n = np.zeros(64, np.int32), np.zeros(64, np.int32), _INT()
+        check(lib().tsl_engine_graphs(self.handle, rows.ctypes.data, ids.ctypes.data, 64, ctypes.byref(n)))
+        return dict(zip(rows[:n.value].tolist(), ids[:n.value].tolist()))
 
     def profile(self, on):
         """Gpu::profile: time every launch on its own (graphs off) from now."""

@@ -200,11 +200,17 @@ struct Engine {
         return 0;
     }
 
-    // Engine::mm (src/llm/engine.rs:233-270): with tuning on, every
-    // candidate is timed (3 warm-up launches, then 10) on the engine's own
-    // buffers and the fastest kept.
+    // Engine::mm (src/llm/engine.rs:233-270). The reference times each tile
+    // configuration of mm_candidates and keeps the fastest. Here the llm
+    // projections' launchers choose their tiles from the shape (decode-sized
+    // rows: the weight-streaming skinny kernel with its K split; prompt-sized
+    // rows: the 64x128 / 128x128 / 256x128 MFMA tiles and K slices), and
+    // the BM/BN/BK of a candidate's meta only enters its cache key: every
+    // candidate is the same code. So the default candidate is specialised
+    // once, nothing is timed, and `tune` changes nothing.
     int mm(const char* name, const std::vector<std::vector<int64_t>>& shapes, bool two, const std::vector<Arg>& args,
            int* out) {
+        (void)args;
         std::ostringstream key;
         key << name << " [";
         for (size_t i = 0; i < shapes.size(); i++) {
@@ -220,26 +226,7 @@ struct Engine {
         }
         auto cands = mm_candidates((size_t)shapes[0][0], two);
         int pick = -1;
-        if (!tune) {
-            TRY(kernel(name, shapes, cands[0].first, cands[0].second, &pick));
-        } else {
-            float best = 1e30f;
-            std::vector<uint64_t> raw;
-            for (auto& a : args) raw.push_back(a.v);
-            for (auto& c : cands) {
-                int k;
-                if (kernel(name, shapes, c.first, c.second, &k)) continue;
-                bool ok = true;
-                for (int i = 0; i < 3 && ok; i++) ok = tsl_launch(k, raw.data(), (int)raw.size()) == 0;
-                float ms = 0;
-                if (ok) ok = tsl_time_launches(k, raw.data(), (int)raw.size(), 10, &ms) == 0;
-                if (ok && ms < best) {
-                    best = ms;
-                    pick = k;
-                }
-            }
-            if (pick < 0) return tsl_fail(TSL_ERR_ARG, key.str() + ": no configuration ran");
-        }
+        TRY(kernel(name, shapes, cands[0].first, cands[0].second, &pick));
         tuned[key.str()] = pick;
         *out = pick;
         return 0;
@@ -589,6 +576,21 @@ int tsl_engine_profile_rows(int engine, char* out, size_t cap, size_t* len) {
     const std::string s = o.str();
     if (len) *len = s.size();
     if (out && cap > s.size()) std::memcpy(out, s.c_str(), s.size() + 1);
+    return 0;
+}
+
+int tsl_engine_graphs(int engine, int32_t* rows, int32_t* graphs, int cap, int* n) {
+    Engine* e = get(engine);
+    if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
+    int i = 0;
+    for (auto& kv : e->graph) {
+        if (i < cap) {
+            rows[i] = (int32_t)kv.first;
+            graphs[i] = kv.second;
+        }
+        i++;
+    }
+    *n = i;
     return 0;
 }
 

@@ -18,6 +18,7 @@
 #include <map>
 #include <mutex>
 #include <sstream>
+#include <array>
 #include <string>
 #include <vector>
 
@@ -218,6 +219,7 @@ struct State {
     std::vector<tsl_launcher> launchers;
     std::map<std::string, int> by_key;
     std::vector<hipGraphExec_t> graphs;
+    std::vector<std::array<int64_t, 4>> graph_nodes;  // per graph: kernel, memset, memcpy, other nodes
     std::vector<hipEvent_t> events;
     std::string name;
     int cus = 0, mhz = 0;
@@ -539,10 +541,28 @@ int tsl_capture_end(int* graph) {
     hipGraph_t gr;
     hipGraphExec_t ex;
     CHECK(hipStreamEndCapture(g.stream, &gr), "hipStreamEndCapture");
+    // What the recording holds, by node type, before it is instantiated.
+    std::array<int64_t, 4> kinds{};
+    size_t nn = 0;
+    CHECK(hipGraphGetNodes(gr, nullptr, &nn), "hipGraphGetNodes");
+    std::vector<hipGraphNode_t> nodes(nn);
+    if (nn) CHECK(hipGraphGetNodes(gr, nodes.data(), &nn), "hipGraphGetNodes");
+    for (size_t i = 0; i < nn; i++) {
+        hipGraphNodeType t;
+        CHECK(hipGraphNodeGetType(nodes[i], &t), "hipGraphNodeGetType");
+        kinds[t == hipGraphNodeTypeKernel ? 0 : t == hipGraphNodeTypeMemset ? 1 : t == hipGraphNodeTypeMemcpy ? 2 : 3]++;
+    }
     CHECK(hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0), "hipGraphInstantiate");
+    g.graph_nodes.push_back(kinds);
     (void)hipGraphDestroy(gr);
     g.graphs.push_back(ex);
     *graph = (int)g.graphs.size() - 1;
+    return 0;
+}
+
+int tsl_graph_nodes(int graph, int64_t* counts) {
+    if (graph < 0 || graph >= (int)g.graph_nodes.size()) return tsl_fail(TSL_ERR_ARG, "no such graph");
+    for (int i = 0; i < 4; i++) counts[i] = g.graph_nodes[graph][i];
     return 0;
 }
 

@@ -105,6 +105,18 @@ def test_graph_replay_matches_eager(gpu):
     for graphs in (False, True):
         e = T.Engine(cfg, limits(pages=64), w, graphs=graphs)
         outs.append(e.generate(reqs, 3)[0])
+        if graphs:
+            # The recorded decode steps are kernel launches only (no memset
+            # or copy nodes): each layer's QKV, attention (+ merge), o and
+            # down projections with their norms, gate_up; then embed, norm,
+            # final norm, logits and argmax.
+            gs = e.graphs()
+            assert gs
+            for rows, g in gs.items():
+                nodes = T.graph_nodes(g)
+                print(f"decode graph for {rows} rows: {nodes}", flush=True)
+                assert nodes["memset"] == nodes["memcpy"] == nodes["other"] == 0
+                assert nodes["kernel"] >= 5 * cfg.layers + 5
         e.close()
     assert outs[0] == outs[1]
 

@@ -99,15 +99,20 @@ def _mm_args(r, name, m, k, n, wscale=0.1):
 @pytest.mark.parametrize("m", [16, 32, 64])
 @pytest.mark.parametrize("name", MM_CASES)
 def test_every_tuning_candidate(name, m):
-    # tests/llm.rs:108-187: each tile configuration the tuner may pick,
-    # within 1e-2 of the largest output.
+    # tests/llm.rs:108-187: each tile configuration the reference's tuner may
+    # pick, within 1e-2 of the largest output. Here the launchers choose tiles
+    # from the shape, so every candidate's meta (a distinct cache key) runs
+    # the same code: the outputs must also be bit-identical across them.
     _say("mm candidates", name, m)
     r = oracle.Rng(5)
     k, n = 256, 96
     args, want = _mm_args(r, name, m, k, n)
+    first = None
     for meta, warps in T.mm_candidates(m, name == "gate_up"):
         got = T.run("llm", name, [a.copy() for a in args], meta=meta, warps=warps, outputs=[len(args) - 1])
         got = got[len(args) - 1]
+        first = got if first is None else first
+        assert np.array_equal(got.view(np.uint8), first.view(np.uint8)), (name, m, meta)
         scale = np.abs(want).max()
         err = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
         assert err <= 1e-2 * scale, (name, m, meta, warps, err, scale)
@@ -630,6 +635,8 @@ def test_graph_replay_of_kernels_with_scratch():
     T.launch(lin, lb)
     T.launch(dec, db)
     g = T.capture_end()
+    nodes = T.graph_nodes(g)
+    assert nodes["kernel"] >= 2 and nodes["memset"] == nodes["memcpy"] == nodes["other"] == 0, nodes
     other = T.kernel("llm", "linear", [[32, 5632], [2048, 5632], [32, 2048]])
     ob = [T.tensor(x[::-1].copy()), lb[1], T.alloc(32 * 2048 * 2)]
     for i in range(3):
