@@ -1142,6 +1142,7 @@ int big_split(int M, int N, int K) {
     if (M <= 64 || K % 8) return 1;
     const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
     if (tiles >= 256 || tiles == 0) return 1;
+    if ((long)((M + 63) / 64) * ((N + 63) / 64) >= 256) return 1;  // 64 x 64 tiles fill the CUs (gemm_dispatch)
     const int nst = (K + 63) / 64;
     return std::max(1, std::min((int)((256 + tiles - 1) / tiles), nst / 32));
 }
@@ -1248,6 +1249,17 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             return TSL_LAUNCHED(what);
         }
     }
+    if constexpr (BT && !DUAL) {
+        if (aligned && M > 64 && tiles(128, 128) < 256 && tiles(64, 64) >= 256) {
+            // X W^T at prefill sizes (the engine's 1024-row qkv, o and down):
+            // 64 x 64 tiles of 4 wavefronts and 3 stages fill every CU without
+            // a K split. 1024 x 2048 x 2048: 23.8 -> 18.7 us; x 5632 (split
+            // 2 + reduce before): 47.4 -> 42.8; 1024 x 2560 x 2048: 23.0 -> 22.1.
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 64, 2, 2, 64, 3>), dim3(tiles(64, 64)), dim3(256), 0, s, A, B, B2, C,
+                               bias, M, N, K, 4);
+            return TSL_LAUNCHED(what);
+        }
+    }
     if (aligned && M > 64 && (BT || !DUAL)) {
         const int split = part ? big_split(M, N, K) : 1;
         if (split > 1) {  // 128 x 128 tiles over K slices, then the ordered sum
@@ -1256,6 +1268,11 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             const long mn = (long)M * N;
             hipLaunchKernelGGL(skinny_reduce<EPI>, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, split, M,
                                N, C, bias);
+        } else if (tiles(128, 128) >= 256 && !BT) {
+            // matmul (B [K, N]) at 128 x 128: 8 wavefronts of 64 x 32 and 3
+            // stages (2048^3: 30.0 -> 26.5 us against 4 wavefronts, 2 stages).
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 4, 64, 3>), dim3(tiles(128, 128)), dim3(512), 0, s, A, B, B2,
+                               C, bias, M, N, K, 4);
         } else if (tiles(128, 128) >= 256) {
             hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);

@@ -455,6 +455,76 @@ TSL_DEV void kv_write_elem(const RopeArgs& a, long e) {
     }
 }
 
+// rope_q and kv_write together, 8 columns per thread: item e = (t, head
+// slot hh of the H query, G key and G value heads of QKV's row, chunk c of
+// D2 / 8). Query and key slots rotate columns 8c .. 8c+7 with their D2
+// partners (16-byte loads and stores, the same rope_rotate arithmetic as
+// the element kernels, so the same bits); value slots copy both chunks. For
+// D = 2 D2, D2 % 8 == 0, W = (H + 2 G) D and 32-bit indices.
+__global__ __launch_bounds__(256) void rope_kv_vec(RopeArgs a, int n) {
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= n) return;
+    const int nc = a.D2 / 8, slots = a.H + 2 * a.G;
+    const int c = e % nc, hh = (e / nc) % slots, t = e / (nc * slots);
+    const int i0 = 8 * c;
+    const u16* row = a.QKV + (size_t)t * a.W + hh * a.D;
+    const u32x4 v1 = *reinterpret_cast<const u32x4*>(row + i0), v2 = *reinterpret_cast<const u32x4*>(row + a.D2 + i0);
+    const int at = a.slot ? a.slot[t] : -1;
+    const bool ain = at >= 0 && at < a.NS;
+    if (hh >= a.H + a.G) {  // a value head: copied
+        const int g = hh - a.H - a.G;
+        u16* vv = a.V + ((size_t)t * a.G + g) * a.D;
+        *reinterpret_cast<u32x4*>(vv + i0) = v1;
+        *reinterpret_cast<u32x4*>(vv + a.D2 + i0) = v2;
+        if (ain) {
+            u16* vc = a.Vc + ((size_t)at * a.G + g) * a.D;
+            *reinterpret_cast<u32x4*>(vc + i0) = v1;
+            *reinterpret_cast<u32x4*>(vc + a.D2 + i0) = v2;
+        }
+        return;
+    }
+    const int p = a.pos[t];
+    const bool pin = p >= 0 && p < a.NPOS;
+    float cs[8], sn[8];
+    if (pin) {
+        const float4v* cp = reinterpret_cast<const float4v*>(a.Cs + (size_t)p * a.D2 + i0);
+        const float4v* sp = reinterpret_cast<const float4v*>(a.Sn + (size_t)p * a.D2 + i0);
+        const float4v c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            cs[j] = c0[j], cs[4 + j] = c1[j];
+            sn[j] = s0[j], sn[4 + j] = s1[j];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) cs[j] = sn[j] = 0.0f;
+    }
+    u32x4 y1, y2;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        u16 a1, a2, b1, b2;
+        rope_rotate(h2f((u16)(v1[j] & 0xffff)), h2f((u16)(v2[j] & 0xffff)), cs[2 * j], sn[2 * j], a1, a2);
+        rope_rotate(h2f((u16)(v1[j] >> 16)), h2f((u16)(v2[j] >> 16)), cs[2 * j + 1], sn[2 * j + 1], b1, b2);
+        y1[j] = (uint32_t)a1 | ((uint32_t)b1 << 16);
+        y2[j] = (uint32_t)a2 | ((uint32_t)b2 << 16);
+    }
+    if (hh < a.H) {
+        u16* q = a.Q + ((size_t)t * a.H + hh) * a.D;
+        *reinterpret_cast<u32x4*>(q + i0) = y1;
+        *reinterpret_cast<u32x4*>(q + a.D2 + i0) = y2;
+        return;
+    }
+    const int g = hh - a.H;
+    u16* kk = a.K + ((size_t)t * a.G + g) * a.D;
+    *reinterpret_cast<u32x4*>(kk + i0) = y1;
+    *reinterpret_cast<u32x4*>(kk + a.D2 + i0) = y2;
+    if (ain) {
+        u16* kc = a.Kc + ((size_t)at * a.G + g) * a.D;
+        *reinterpret_cast<u32x4*>(kc + i0) = y1;
+        *reinterpret_cast<u32x4*>(kc + a.D2 + i0) = y2;
+    }
+}
+
 // KIND 0: rope_q, 1: kv_write, 2: both (the engine's fused step; the index
 // space of rope_q first, then kv_write's).
 template <int KIND>
@@ -680,6 +750,16 @@ int launch_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
     r.Q = P<u16>(a[5]), r.Kc = P<u16>(a[6]), r.Vc = P<u16>(a[7]), r.K = P<u16>(a[8]), r.V = P<u16>(a[9]);
     const long nq = (long)r.T * r.H * r.D2, nkv = (long)r.T * r.G * std::max(r.D2, r.D);
     if (nq + nkv == 0) return 0;
+    const long nvec = (long)r.T * (r.H + 2 * r.G) * (r.D2 / 8);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(r.QKV) | reinterpret_cast<uintptr_t>(r.Q) |
+                           reinterpret_cast<uintptr_t>(r.Kc) | reinterpret_cast<uintptr_t>(r.Vc) |
+                           reinterpret_cast<uintptr_t>(r.K) | reinterpret_cast<uintptr_t>(r.V) |
+                           reinterpret_cast<uintptr_t>(r.Cs) | reinterpret_cast<uintptr_t>(r.Sn)) & 15) == 0;
+    if (aligned && r.D == 2 * r.D2 && r.D2 % 8 == 0 && r.W == (r.H + 2 * r.G) * r.D && (long)r.T * r.W < (1L << 31) &&
+        (long)r.NS * r.G * r.D < (1L << 31) && (long)r.NPOS * r.D2 < (1L << 31)) {
+        hipLaunchKernelGGL(rope_kv_vec, dim3((unsigned)((nvec + 255) / 256)), dim3(256), 0, s, r, (int)nvec);
+        return TSL_LAUNCHED("rope_kv");
+    }
     hipLaunchKernelGGL(rope_kernel<2>, dim3(grid1(nq + nkv)), dim3(256), 0, s, r, nq, nkv);
     return TSL_LAUNCHED("rope_kv");
 }

@@ -602,9 +602,14 @@ def test_rope_and_kv_write(cfgname):
     untouched = [i for i in range(NS) if i not in set(slot[:Tn - 2].tolist())]
     np.testing.assert_array_equal(out[5][untouched], Kc[untouched])
     # The engine's fused launch (fused/rope_kv) writes exactly what the two do.
-    fz = T.run("fused", "rope_kv", [qkv, pos, slot, c, s, np.zeros((Tn, H, D), np.float16), Kc, Vc, K, V])
-    for got, ref in ((fz[5], q), (fz[6], out[5]), (fz[7], out[6]), (fz[8], out[7]), (fz[9], out[8])):
-        np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
+    # (It takes 8 columns per thread when D = 2 D2 with D2 % 8 == 0, as both
+    # configs here; positions outside the tables rotate by zeros.)
+    for pp in (pos, np.where(np.arange(Tn) % 5 == 3, cfg.max_pos + 3, pos).astype(np.int32)):
+        q = T.run("llm", "rope_q", [qkv, pp, c, s, np.zeros((Tn, H, D), np.float16)], outputs=[4])[4]
+        out = T.run("llm", "kv_write", [qkv, pp, slot, c, s, Kc, Vc, K, V])
+        fz = T.run("fused", "rope_kv", [qkv, pp, slot, c, s, np.zeros((Tn, H, D), np.float16), Kc, Vc, K, V])
+        for got, ref in ((fz[5], q), (fz[6], out[5]), (fz[7], out[6]), (fz[8], out[7]), (fz[9], out[8])):
+            np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
 
 
 # ---------------------------------------------------------------- graph replay
