@@ -15,8 +15,10 @@ events on the library's stream, bracketed by stream synchronisation.
                 paged GQA decode (GB/s against 8 TB/s), paged_attention (G = H),
                 the engine's prefill_attention and its five projections at
                 decode (32 rows, GB/s) and prefill (1024 rows, TFLOP/s) sizes,
-                RMSNorm and softmax 4096^2, and TinyLlama-shape decode tokens/s
-                (skip with --no-llm).
+                RMSNorm and softmax 4096^2, TinyLlama-shape decode tokens/s
+                (skip with --no-llm), and calibration probes (the matrix
+                cores' sustained rate on random against near-constant f16,
+                the streaming-read floor at the engine's kernel sizes).
 """
 
 import argparse
@@ -383,7 +385,7 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="TinyLlama case: launch decode steps kernel by kernel (for kernel traces)")
     ap.add_argument("--only", default="", help="comma list of cases: gemm1024,gemm2048,fa512..fa4096,decode,paged,"
-                    "prefill,proj,"
+                    "prefill,proj,probes,"
                     "rmsnorm,softmax,llm,copy (counter calibration); 'none' for the headline GEMM alone")
     ap.add_argument("--profile", action="store_true",
                     help="few launches, no clock warm-up: for rocprofv3 counter passes")
@@ -493,6 +495,24 @@ def main():
             m = t.median(20)
             cases.append({"case": "add f32 32Mi (reads 256 MiB, writes 128 MiB)", "ms": round(m, 5),
                           "gbps": round(12.0 * n / m / 1e6, 1)})
+        if want("probes"):
+            # Calibration, not bench lines: what the matrix cores sustain on the
+            # GEMM's MFMA pattern with random against nearly constant operands
+            # (the clock drops under the power limit with random data), and the
+            # streaming-read floor at the sizes of the engine's kernels.
+            for rnd in (False, True):
+                for reads in (False, True):
+                    tf = T.probe_mfma(rnd, reads)
+                    cases.append({"case": "probe: mfma 32x32x16 f16, " + ("random" if rnd else "near-constant") +
+                                  " operands" + (", with the GEMM's LDS operand reads" if reads else ""),
+                                  "tflops": round(tf, 1), "frac_mfma": round(tf / PEAK_MFMA_F16, 4)})
+            big = T.alloc(1 << 30)
+            T.write(big, 0, np.ones(1 << 28, np.float32))
+            for mb in (10, 23, 46, 131, 512):
+                gbs = T.probe_stream(big, mb << 20)
+                cases.append({"case": f"probe: streaming read of {mb} MiB", "us": round((mb << 20) / gbs / 1e3, 2),
+                              "gbps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4)})
+            T.free(big)
         for kind in ("rmsnorm", "softmax"):
             if not want(kind):
                 continue

@@ -126,6 +126,20 @@ int tsl_event_elapsed(int start, int end, float* ms);
 int tsl_decode_attention_noalloc(uint64_t q, uint64_t kc, uint64_t vc, uint64_t table, uint64_t lens, uint64_t o,
                                  float scale, int B, int H, int G, int D, int NP, int P, int MP);
 
+/* ---- calibration probes (no reference counterpart: they measure what this
+ * GPU sustains on the hot path's building blocks, for the roofline notes) */
+
+/* TFLOP/s of v_mfma_f32_32x32x16_f16 issued back to back by 8 wavefronts per
+ * CU (the GEMM's occupancy and 8 accumulators per wave, a workgroup barrier
+ * every 32 MFMAs), operands random f16 (random = 1) or nearly constant, with
+ * or without the GEMM's LDS operand reads (lds_reads = 1). One launch of
+ * iters iterations after a warm-up launch. */
+int tsl_probe_mfma(int random, int lds_reads, int iters, double* tflops);
+/* GB/s of iters back-to-back streaming reads of bytes each (512 workgroups,
+ * four 16-byte loads in flight per lane), launch i reading window i (mod the
+ * windows that fit) of the buf_bytes at device address buf. */
+int tsl_probe_stream(uint64_t buf, size_t buf_bytes, size_t bytes, int iters, double* gbps);
+
 /* ---- the LLM engine (src/llm/engine.rs, src/llm/sched.rs, src/llm/mod.rs) */
 
 /* Config (src/llm/mod.rs:15-28). */

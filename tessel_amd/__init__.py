@@ -49,7 +49,7 @@ EXPORTS = [
     "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
     "tsl_checkpoint_save", "tsl_json_roundtrip", "tsl_rng_new", "tsl_rng_bits", "tsl_rng_tensor",
     "tsl_time_each", "tsl_engine_profile", "tsl_engine_profile_rows", "tsl_schedule_trace",
-    "tsl_graph_nodes", "tsl_engine_graphs",
+    "tsl_graph_nodes", "tsl_engine_graphs", "tsl_probe_mfma", "tsl_probe_stream",
     "tsl_decode_attention_noalloc",
 ]
 
@@ -116,6 +116,8 @@ def _declare(L):
     L.tsl_engine_step.argtypes = [_INT, _INT, _P, _P, _P, _INT, _P, _INT, _P, _P, _INT, _P, _P]
     L.tsl_generate.argtypes = [_INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, ctypes.POINTER(Stats), _P]
     L.tsl_graph_nodes.argtypes = [_INT, _P]
+    L.tsl_probe_mfma.argtypes = [_INT, _INT, _INT, ctypes.POINTER(ctypes.c_double)]
+    L.tsl_probe_stream.argtypes = [_U64, ctypes.c_size_t, ctypes.c_size_t, _INT, ctypes.POINTER(ctypes.c_double)]
     L.tsl_engine_graphs.argtypes = [_INT, _P, _P, _INT, ctypes.POINTER(_INT)]
     L.tsl_decode_attention_noalloc.argtypes = [_U64] * 6 + [ctypes.c_float] + [_INT] * 7
     L.tsl_schedule_trace.argtypes = [ctypes.POINTER(Limits), _INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, _P,
@@ -313,6 +315,23 @@ def graph_nodes(g):
     c = np.zeros(4, np.int64)
     check(lib().tsl_graph_nodes(int(g), c.ctypes.data))
     return dict(zip(("kernel", "memset", "memcpy", "other"), c.tolist()))
+
+
+def probe_mfma(random, lds_reads, iters=2000):
+    """TFLOP/s the matrix cores sustain on the GEMM's MFMA pattern (a
+    calibration probe: random or nearly constant f16 operands, with or
+    without the GEMM's LDS operand reads)."""
+    v = ctypes.c_double()
+    check(lib().tsl_probe_mfma(int(random), int(lds_reads), int(iters), ctypes.byref(v)))
+    return v.value
+
+
+def probe_stream(buf, nbytes, iters=40):
+    """GB/s of back-to-back streaming reads of nbytes each, cycling through
+    the windows of device buffer buf."""
+    v = ctypes.c_double()
+    check(lib().tsl_probe_stream(buf.ptr, buf.bytes, int(nbytes), int(iters), ctypes.byref(v)))
+    return v.value
 
 
 def event_record():

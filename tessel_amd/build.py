@@ -21,7 +21,7 @@ HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-Wall", "-
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-mf16c"]  # f16 conversions in hardware
 
-SOURCES = ["runtime.hip", "gemm.hip", "attention.hip", "decode.hip", "rows.hip"]
+SOURCES = ["runtime.hip", "gemm.hip", "attention.hip", "decode.hip", "rows.hip", "probe.hip"]
 HOST_SOURCES = ["engine.cpp", "checkpoint.cpp"]
 
 

@@ -1,0 +1,183 @@
+// Calibration probes for the roofline figures (not .tl kernels; bench.py's
+// --only probes runs them): what this MI355X sustains on the operations the
+// hot-path kernels are built from, measured the same way the kernels are.
+//
+//   tsl_probe_mfma    v_mfma_f32_32x32x16_f16 back to back, 2 wavefronts per
+//                     SIMD on every CU (the GEMM's occupancy and accumulator
+//                     layout: 8 independent 32x32 tiles per wave), operands
+//                     either constant-like (few toggling bits) or random f16,
+//                     optionally with the GEMM's per-k-step LDS operand reads
+//                     (4 ds_read_b128 + 4 ds_read_b64_tr_b16 per 8 MFMAs)
+//   tsl_probe_stream  streaming reads by 512 workgroups, four 16-byte loads
+//                     in flight per lane, each launch a new window of a large
+//                     buffer: the HBM floor (launch included) of a kernel
+//                     that must read that many bytes
+#include "common.h"
+
+#include "../../include/tessel.h"
+
+namespace {
+
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 fp16x4_t;
+
+TSL_DEV half4 probe_tr(const char* p) {
+    fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) fp16x4_t*)(p));
+    return __builtin_bit_cast(half4, v);
+}
+
+template <bool READS, bool RANDOM>
+__global__ __launch_bounds__(512, 1) void probe_mfma_kernel(float* out, int n) {
+    __shared__ __attribute__((aligned(16))) char lds[131072];
+    for (int i = threadIdx.x; i < 131072 / 2; i += blockDim.x) {
+        uint32_t h = (uint32_t)i * 2654435761u ^ (blockIdx.x * 40503u);
+        h ^= h >> 13;
+        h *= 0x5bd1e995u;
+        h ^= h >> 15;
+        reinterpret_cast<half_t*>(lds)[i] =
+            RANDOM ? (half_t)(((int)(h & 0xffff) - 32768) * (1.0f / 16384.0f)) : (half_t)(1e-3f * (i & 7));
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const char* pa = lds + (wave & 1) * 16384 + lane * 16;
+    const char* pb = lds + 65536 + (wave >> 1) * 4096 + lane * 8;
+    half8 a0[4], a1[4], b0[2], b1[2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        a0[i] = *reinterpret_cast<const half8*>(pa + i * 4096);
+        a1[i] = *reinterpret_cast<const half8*>(pa + i * 4096 + 2048);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        b0[j] = *reinterpret_cast<const half8*>(pa + 32768 + j * 1024);
+        b1[j] = *reinterpret_cast<const half8*>(pa + 33792 + j * 1024);
+    }
+    float16v acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = float16v{};
+    for (int it = 0; it < n; it++) {
+        __syncthreads();  // the GEMM's once-per-k-step barrier
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            half8* av = (st & 1) ? a1 : a0;
+            half8* bv = (st & 1) ? b1 : b0;
+            half8* an = (st & 1) ? a0 : a1;
+            half8* bn = (st & 1) ? b0 : b1;
+            if constexpr (READS) {
+                const int so = ((it + st) & 1) * 32768 + st * 64;
+#pragma unroll
+                for (int i = 0; i < 4; i++) an[i] = *reinterpret_cast<const half8*>(pa + so + i * 4096);
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const half4 h0 = probe_tr(pb + so + j * 1024), h1 = probe_tr(pb + so + j * 1024 + 512);
+                    bn[j] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+            if constexpr (READS) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            }
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) s += acc[i][j][r];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+__global__ __launch_bounds__(512) void probe_stream_kernel(const u32x4* __restrict__ p, size_t n16,
+                                                           uint32_t* __restrict__ out) {
+    constexpr int U = 4;
+    const size_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const size_t beg = (size_t)blockIdx.x * per, end = beg + per < n16 ? beg + per : n16;
+    u32x4 acc = {0, 0, 0, 0};
+    for (size_t i = beg + threadIdx.x; i < end; i += 512 * U) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            v[u] = i + u * 512 < end ? __builtin_nontemporal_load(p + i + u * 512) : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u];
+    }
+    if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x9e3779b9u) out[0] = 1;  // keeps the loads
+}
+
+// Milliseconds of `launch` repeated iters times on the library stream.
+template <class F>
+int probe_time(F launch, int iters, float* ms) {
+    hipStream_t s = (hipStream_t)tsl_stream();
+    hipEvent_t a, b;
+    if (tsl_hip_check(hipEventCreate(&a), "probe event") || tsl_hip_check(hipEventCreate(&b), "probe event")) return -1;
+    launch(s);  // warm-up
+    int r = tsl_hip_check(hipEventRecord(a, s), "probe record");
+    for (int i = 0; i < iters && !r; i++) launch(s);
+    if (!r) r = tsl_hip_check(hipEventRecord(b, s), "probe record");
+    if (!r) r = tsl_hip_check(hipEventSynchronize(b), "probe sync");
+    if (!r) r = tsl_hip_check(hipEventElapsedTime(ms, a, b), "probe elapsed");
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return r;
+}
+
+}  // namespace
+
+extern "C" int tsl_probe_mfma(int random, int lds_reads, int iters, double* tflops) {
+    if (iters <= 0 || iters > 1 << 20) return tsl_fail(TSL_ERR_ARG, "probe_mfma: iters in 1 .. 2^20");
+    if (tsl_open()) return -1;
+    const int cus = num_cus();
+    float* out = nullptr;
+    if (tsl_hip_check(hipMalloc(&out, (size_t)cus * 512 * 4), "probe_mfma buffer")) return -1;
+    auto go = [&](hipStream_t s) {
+        if (random && lds_reads) hipLaunchKernelGGL((probe_mfma_kernel<true, true>), dim3(cus), dim3(512), 0, s, out, iters);
+        else if (random) hipLaunchKernelGGL((probe_mfma_kernel<false, true>), dim3(cus), dim3(512), 0, s, out, iters);
+        else if (lds_reads) hipLaunchKernelGGL((probe_mfma_kernel<true, false>), dim3(cus), dim3(512), 0, s, out, iters);
+        else hipLaunchKernelGGL((probe_mfma_kernel<false, false>), dim3(cus), dim3(512), 0, s, out, iters);
+    };
+    float ms = 0.0f;
+    int r = probe_time(go, 1, &ms);
+    if (!r) r = TSL_LAUNCHED("probe_mfma");
+    (void)hipFree(out);
+    if (r) return r;
+    // 8 MFMAs of 32x32x16 (2 x 16384 flops each) per wave per k-step quarter,
+    // 4 quarters per iteration, 8 waves per CU.
+    *tflops = 2.0 * 32 * 32 * 16 * 8 * 4 * 8 * (double)cus * iters / (ms * 1e-3) / 1e12;
+    return 0;
+}
+
+extern "C" int tsl_probe_stream(uint64_t buf, size_t buf_bytes, size_t bytes, int iters, double* gbps) {
+    if (iters <= 0 || bytes < 16 || bytes > buf_bytes)
+        return tsl_fail(TSL_ERR_ARG, "probe_stream: iters >= 1, 16 <= bytes <= buf_bytes");
+    // Consecutive reads take consecutive bytes-sized windows of the buffer,
+    // so a buffer of more than twice the 256 MB last-level cache keeps every
+    // read coming from HBM.
+    const size_t windows = buf_bytes / (bytes / 16 * 16);
+    int w = 0;
+    if (tsl_open()) return -1;
+    uint32_t* out = nullptr;
+    if (tsl_hip_check(hipMalloc(&out, 4), "probe_stream flag")) return -1;
+    auto go = [&](hipStream_t s) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(buf) + (size_t)(w++ % windows) * (bytes / 16);
+        hipLaunchKernelGGL(probe_stream_kernel, dim3(512), dim3(512), 0, s, p, bytes / 16, out);
+    };
+    float ms = 0.0f;
+    int r = probe_time(go, iters, &ms);
+    if (!r) r = TSL_LAUNCHED("probe_stream");
+    (void)hipFree(out);
+    if (r) return r;
+    *gbps = (double)(bytes / 16 * 16) * iters / (ms * 1e-3) / 1e9;
+    return 0;
+}
