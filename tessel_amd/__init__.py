@@ -16,7 +16,9 @@ import struct
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libtessel_hip.so")
+# TSL_LIB selects another build of the same library (the sanitized host
+# build of `python tessel_amd/build.py --sanitize`).
+LIB_PATH = os.environ.get("TSL_LIB") or os.path.join(_HERE, "libtessel_hip.so")
 _lib = None
 
 

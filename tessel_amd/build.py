@@ -55,5 +55,28 @@ def build(verbose=False):
     return LIB
 
 
+def build_sanitized():
+    """tessel_amd/libtessel_hip_asan.so: the host sources (engine, checkpoint)
+    built with AddressSanitizer and UndefinedBehaviorSanitizer, linked with
+    the normal GPU objects (GPU sanitizers are not available on the GPU
+    pool). For CPU test runs with the ASan runtime preloaded:
+
+        LD_PRELOAD=$(clang -print-file-name=libclang_rt.asan-x86_64.so) \
+        ASAN_OPTIONS=detect_leaks=0 UBSAN_OPTIONS=halt_on_error=1 \
+        TSL_LIB=tessel_amd/libtessel_hip_asan.so python -m pytest tests -m "not gpu"
+    """
+    build()
+    san = ["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined"]
+    objs = []
+    for s in HOST_SOURCES:
+        o = os.path.join(BUILD, s.replace(".cpp", ".asan.o"))
+        _compile([CXX] + HOST_FLAGS + san + ["-c", os.path.join(CSRC, s), "-o", o])
+        objs.append(o)
+    objs += [os.path.join(BUILD, s.replace(".hip", ".o")) for s in SOURCES]
+    out = os.path.join(HERE, "libtessel_hip_asan.so")
+    _compile([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-fsanitize=address,undefined", "-o", out] + objs)
+    return out
+
+
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build_sanitized() if "--sanitize" in sys.argv else build(verbose=True))
