@@ -271,6 +271,42 @@ TSL_DEV half4 lds_read_tr(const u16* p) {
     return __builtin_bit_cast(half4, v);
 }
 
+// The epilogue of one 32x32 accumulator tile (lane l: column col = .. + l % 32,
+// register r: row row0 + 8 (r / 4) + 4 (l / 32) + r % 4) for the plain
+// epilogues: f16, f32, R += ., + bias. Rows past M and columns past N are
+// dropped.
+template <int EPI>
+TSL_DEV void store_acc32(void* C, const u16* bias, int M, int N, int row0, int col, int g, const float16v& acc) {
+    if (col >= N) return;
+    // The residual's 16 old values, all loads in flight before any store (the
+    // compiler cannot tell the stores from the loads apart, so an
+    // interleaved read-add-write runs serially).
+    float old[EPI == EPI_RESID ? 16 : 1];
+    if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = row0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            old[r] = row < M ? reinterpret_cast<const float*>(C)[(size_t)row * N + col] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int row = row0 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (row >= M) continue;
+        const size_t o = (size_t)row * N + col;
+        const float v = acc[r];
+        if constexpr (EPI == EPI_F16) {
+            reinterpret_cast<u16*>(C)[o] = f2h(v);
+        } else if constexpr (EPI == EPI_F32) {
+            reinterpret_cast<float*>(C)[o] = v;
+        } else if constexpr (EPI == EPI_RESID) {
+            reinterpret_cast<float*>(C)[o] = old[r] + v;
+        } else if constexpr (EPI == EPI_BIAS) {
+            reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
+        }
+    }
+}
+
 // The compute of a K step is software pipelined: the MFMA operands of
 // k-step s+1 are read from LDS while the 16 MFMAs of step s run.
 //
@@ -496,22 +532,15 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const int col = n0 + wn0 + j * 32 + (lane & 31);
-            if (col >= N) continue;
-            // The residual's 16 old values of this tile, all loads in flight
-            // before any store (the compiler cannot tell the stores from the
-            // loads apart, so an interleaved read-add-write runs serially).
-            float old[EPI == EPI_RESID && !SPLIT ? 16 : 1];
-            if constexpr (EPI == EPI_RESID && !SPLIT) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    old[r] = row < M ? reinterpret_cast<const float*>(C)[(size_t)row * N + col] : 0.0f;
-                }
+            const int row0 = m0 + wm0 + i * 32, col = n0 + wn0 + j * 32 + (lane & 31);
+            if constexpr (!SPLIT && !DUAL) {
+                store_acc32<EPI>(C, bias, M, N, row0, col, g, acc[i][j]);
+                continue;
             }
+            if (col >= N) continue;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                const int row = row0 + 8 * (r >> 2) + 4 * g + (r & 3);
                 if (row >= M) continue;
                 const size_t o = (size_t)row * N + col;
                 const float v = acc[i][j][r];
@@ -520,20 +549,183 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
                     float* pp = part + (size_t)ks * (DUAL ? 2 : 1) * mn + o;
                     pp[0] = v;
                     if constexpr (DUAL) pp[mn] = acc2[DUAL ? i : 0][DUAL ? j : 0][r];
-                } else if constexpr (EPI == EPI_F16) {
-                    reinterpret_cast<u16*>(C)[o] = f2h(v);
-                } else if constexpr (EPI == EPI_F32) {
-                    reinterpret_cast<float*>(C)[o] = v;
-                } else if constexpr (EPI == EPI_RESID) {
-                    reinterpret_cast<float*>(C)[o] = old[r] + v;
-                } else if constexpr (EPI == EPI_BIAS) {
-                    reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
                 } else {
                     const float u = acc2[DUAL ? i : 0][DUAL ? j : 0][r];
                     reinterpret_cast<u16*>(C)[o] = f2h(v / (1.0f + expf(-v)) * u);
                 }
             }
         }
+}
+
+// The 256 x 256 tile for large products (K % 64 == 0), as a ping-pong of
+// two wavefront groups. 8 wavefronts of 128 x 64 (WGM 2 x WGN 4, as
+// gemm_big's 256 x 256); group 0 (waves 0-3) and group 1 (waves 4-7) put one
+// wavefront on each SIMD and take turns, separated by workgroup barriers:
+// while one group runs a K step's 32 MFMAs back to back from registers, the
+// other reads its next K step's operands from LDS into registers. Group 0
+// also loads the A tile of the next step and group 1 the B tile of the step
+// after that, so the direct-to-LDS writes are spread over both groups'
+// read phases. LDS is gemm_big's 2-stage layout and swizzle.
+//
+// Phase p (between barriers p and p + 1): group 0 reads step p/2 (p even)
+// or computes step (p-1)/2 (p odd); group 1 is one phase behind. A stage's
+// A (B) tile is rewritten only after both groups' reads of its previous step,
+// and every load has landed (its issuing wave's vmcnt, then a barrier) before
+// the phase that reads it: A of step s + 1 is issued at the start of group
+// 0's read of step s and waited for at the end of its compute of step s; B
+// of step s + 2 is issued by group 1 right after its read of step s and
+// waited for at the end of its read of step s + 1.
+template <bool BT, int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, const u16* __restrict__ B,
+                                                  void* __restrict__ C, const u16* __restrict__ bias, int M, int N,
+                                                  int K, int G) {
+    constexpr int BM = 256, BN = 256, BK = 64, WGN = 4, KC = BK / 8;
+    constexpr int WM = 128, WN = 64, TM = WM / 32, TN = WN / 32;
+    constexpr int LP = BM * BK / 512 / 4;  // 1 KB loads per wavefront per step (of A in group 0, of B in group 1)
+    constexpr int RPL = 512 / BN, RPA = 512 / BK;
+    constexpr int STAGE = (BM + BN) * BK * 2;
+    __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE / 2];
+    auto sw = [](int r) { return (r >> 1) & 7; };
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave >> 2, w4 = wave & 3;
+    const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+    int tm, tn;
+    tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, (N + BN - 1) / BN, G, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int g = lane >> 5;
+    const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
+
+    // This wavefront's loads: 1 KB each of the A tile (group 0) or the B
+    // tile (group 1), lane offsets relative to the step's first column (A,
+    // W) or row (B [K, N]); the buffer base advances with k in scalars.
+    uint32_t off[LP];
+#pragma unroll
+    for (int i = 0; i < LP; i++) {
+        const int q = w4 * LP + i;
+        if (grp == 0 || BT) {
+            const int r = RPA * q + lane / KC, c = (lane % KC) ^ sw(r);
+            const int lim = grp == 0 ? M - m0 : N - n0, base = grp == 0 ? m0 : n0;
+            off[i] = r < lim ? (uint32_t)(((base + r) * K + 8 * c) * 2) : (uint32_t)OOB;
+        } else {
+            const int rk = RPL * q + lane / (BN / 8), cb = (lane % (BN / 8)) ^ ((rk & 3) << 2), n = n0 + 8 * cb;
+            off[i] = n < N ? (uint32_t)((rk * N + n) * 2) : (uint32_t)OOB;
+        }
+    }
+    auto issue = [&](int k0, int stage) {
+        const bool a = grp == 0;
+        const long shift = a || BT ? (long)k0 * 2 : (long)k0 * N * 2;
+        const char* base = reinterpret_cast<const char*>(a ? A : B) + shift;
+        i32x4 rs = make_rsrc(base, (uint32_t)((a ? (long)M * K : (long)N * K) * 2 - shift));
+#pragma unroll
+        for (int c = 0; c < 4; c++) rs[c] = __builtin_amdgcn_readfirstlane(rs[c]);  // uniform: keep it in SGPRs
+        const uint32_t dst =
+            __builtin_amdgcn_readfirstlane(lds_base + stage * STAGE + (a ? 0 : BM * BK * 2) + w4 * LP * 1024);
+#pragma unroll
+        for (int i = 0; i < LP; i++)
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(dst + i * 1024),
+                         "v"(off[i]), "s"(rs));
+    };
+
+    // LDS byte addresses of this lane's operands in stage 0 (gemm_big's).
+    uint32_t a_addr[BK / 16], b_addr[TN];
+#pragma unroll
+    for (int st = 0; st < BK / 16; st++) {
+        const int r = wm0 + (lane & 31);
+        a_addr[st] = (uint32_t)((r * KC + ((2 * st + g) ^ sw(r))) * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        if constexpr (BT) {
+            b_addr[j] = (uint32_t)(BM * BK * 2 + (wn0 + j * 32 + (lane & 31)) * KC * 16);
+        } else {
+            const int jj = lane & 15;
+            const int n = wn0 + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (jj & 3), k = 8 * g + (jj >> 2);
+            b_addr[j] = (uint32_t)(BM * BK * 2 + k * BN * 2 + ((((n >> 3) ^ ((k & 3) << 2)) << 3) + (n & 7)) * 2);
+        }
+    }
+    const char* ldsc = reinterpret_cast<const char*>(lds);
+    half8 av[BK / 16][TM], bv[BK / 16][TN];
+    auto read_step = [&](int stage) {
+        const int so = stage * STAGE;
+#pragma unroll
+        for (int st = 0; st < BK / 16; st++) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                av[st][i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 32 * BK * 2);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                if constexpr (BT) {
+                    const int r = wn0 + j * 32 + (lane & 31);
+                    bv[st][j] = *reinterpret_cast<const half8*>(ldsc + so + b_addr[j] + (((2 * st + g) ^ sw(r)) * 16));
+                } else {
+                    const u16* p = reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + 16 * st * BN * 2);
+                    bv[st][j] = __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * BN), 0, 1, 2, 3, 4, 5, 6, 7);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the operands are in registers
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    float16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = float16v{};
+    auto compute = [&]() {
+#pragma unroll
+        for (int st = 0; st < BK / 16; st++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[st][i], bv[st][j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // A workgroup barrier that nothing is scheduled across (LDS reads and
+    // MFMAs stay in their phase).
+    auto bar = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Both groups execute 2 nk + 1 barriers.
+    const int nk = K / BK;
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    bar();
+    if (grp == 0) {
+        for (int s = 0; s < nk; s++) {
+            if (s + 1 < nk) issue((s + 1) * BK, (s + 1) & 1);
+            read_step(s & 1);
+            bar();
+            compute();
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // A of step s + 1 has landed
+            bar();
+        }
+    } else {
+        if (nk > 1) issue(BK, 1);
+        bar();
+        for (int s = 0; s < nk; s++) {
+            read_step(s & 1);
+            if (s + 2 < nk) {
+                issue((s + 2) * BK, s & 1);
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(LP));  // B of step s + 1 has landed
+            } else {
+                __builtin_amdgcn_s_waitcnt(0x0f70);
+            }
+            bar();
+            compute();
+            if (s + 1 < nk) bar();
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            store_acc32<EPI>(C, bias, M, N, m0 + wm0 + i * 32, n0 + wn0 + j * 32 + (lane & 31), g, acc[i][j]);
 }
 
 // matmul_f32 (kernels/matmul.tl:19-27): f32 operands through LDS, f32 FMA.
@@ -1233,9 +1425,13 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
     if constexpr (!DUAL) {
         if (tiles(256, 256) >= 224 && aligned) {
             // 8 wavefronts of 128 x 64 (2 per SIMD, 128 accumulator registers
-            // each): one wave's MFMAs cover the other's loads and barrier.
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4, 64, 2>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, B2,
-                               C, bias, M, N, K, 4);
+            // each): the ping-pong form when K is whole steps, else one
+            // wave's MFMAs cover the other's loads and barrier.
+            if (K % 64 == 0)
+                hipLaunchKernelGGL((gemm_pp<BT, EPI>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, C, bias, M, N, K, 4);
+            else
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4, 64, 2>), dim3(tiles(256, 256)), dim3(512), 0, s, A,
+                                   B, B2, C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
     }

@@ -65,6 +65,41 @@ def test_matmul_large_sampled(n):
     parity("matmul rows", got[rows], want_rows)
 
 
+@pytest.mark.parametrize("m,k,n", [(3900, 1024, 4000), (4000, 1000, 3900)])
+def test_matmul_large_tiles_ragged_exact(m, k, n):
+    # The 256 x 256 tiles with ragged M and N: the ping-pong form (K % 64 == 0)
+    # and the two-stage form (a partial last K step). Integer operands make
+    # every f32 sum exact, so the f16 outputs must equal the rounded integers.
+    _say("matmul large tiles", m, k, n)
+    rng = np.random.default_rng(m + k)
+    a = rng.integers(-3, 4, (m, k)).astype(np.float16)
+    b = rng.integers(-3, 4, (k, n)).astype(np.float16)
+    want = (a.astype(np.float32) @ b.astype(np.float32)).astype(np.float16)
+    got = T.run("matmul", "matmul", [a, b, np.zeros((m, n), np.float16)], outputs=[2])[2]
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("name", ["linear", "linear_residual", "logits"])
+def test_llm_matmuls_large_tiles_ragged(name):
+    # X W^T on the 256 x 256 ping-pong tiles (ragged M and N) with each plain
+    # epilogue, against f64.
+    _say("llm mm large tiles", name)
+    m, k, n = 3900, 512, 4000
+    r = oracle.Rng(900)
+    x = r.tensor("f16", [m, k], 1.0)
+    w = r.tensor("f16", [n, k], 1.0 / np.sqrt(k))
+    prod = x.astype(np.float64) @ w.astype(np.float64).T
+    if name == "linear_residual":
+        res = r.tensor("f32", [m, n], 1.0)
+        args, want = [x, w, res.copy()], res + prod
+    elif name == "logits":
+        args, want = [x, w, np.zeros((m, n), np.float32)], prod
+    else:
+        args, want = [x, w, np.zeros((m, n), np.float16)], prod
+    got = T.run("llm", name, args, outputs=[2])[2]
+    parity(f"{name} {m}x{k}x{n}", got, want)
+
+
 def test_matmul_f32_and_linear_bias():
     _say("matmul_f32, linear")
     r = oracle.Rng(12)
