@@ -1472,6 +1472,11 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
         } else if (tiles(128, 128) >= 256) {
             hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
+        } else if (!BT && tiles(64, 128) < 256 && tiles(32, 128) >= 256) {
+            // matmul with too few 64 x 128 tiles to fill the CUs (1024^3):
+            // 32 x 128 tiles, 4 wavefronts of 32 x 32 (9.05 -> 7.95 us).
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 32, 128, 1, 4, 64, 2>), dim3(tiles(32, 128)), dim3(256), 0, s, A, B, B2,
+                               C, bias, M, N, K, 4);
         } else {  // 64 x 128 tiles (4 wavefronts of 64 x 32): twice the workgroups;
                   // X W^T keeps two K steps in flight (matmul's in-register B
                   // transpose does better with one)
