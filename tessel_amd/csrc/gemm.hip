@@ -1182,7 +1182,12 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
     const int nblk = (N + rpb - 1) / rpb;
     const uint32_t ring = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds) + wave * 2 * SLOT;
 
-    // X operands of this wavefront's steps (rows past M are zero).
+    // X operands of this wavefront's steps (rows past M are zero), loaded
+    // before the W blocks. The loads are written out: the compiler counts
+    // only its own loads, so its wait before the first use would also wait
+    // for every W load issued after them; an explicit vmcnt below leaves the
+    // W loads in flight, and each operand passes through an empty asm after
+    // it, so nothing reads it earlier.
     const u32x4 z = {0, 0, 0, 0};
     u32x4 xv[SPW][MT][2];
 #pragma unroll
@@ -1190,9 +1195,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
 #pragma unroll
         for (int t = 0; t < MT; t++) {
             const bool ok = j < nsw && 16 * t + row < M;
-            const u16* xp = X + (size_t)(ok ? 16 * t + row : 0) * K + kw + 64 * j + 8 * g;
+            const u16* xp = X + (size_t)(ok ? 16 * t + row : 0) * K + kw + 64 * (ok ? j : 0) + 8 * g;
 #pragma unroll
-            for (int i = 0; i < 2; i++) xv[j][t][i] = ok ? ldg16(xp + 32 * i) : z;
+            for (int i = 0; i < 2; i++) asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(xv[j][t][i]) : "v"(xp + 32 * i));
         }
     // W segments of block b into ring slot: load q covers chunks 64 q ..
     // 64 q + 63 (row p / cpr, position p % cpr, holding chunk pos ^ (row & 15)).
@@ -1218,6 +1223,22 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
     const int b0 = blockIdx.x, bs = gridDim.x;
     if (b0 < nblk) load_w(b0, 0);
     if (b0 + bs < nblk) load_w(b0 + bs, 1);
+    {
+        const int wl = (b0 < nblk ? nl : 0) + (b0 + bs < nblk ? nl : 0);  // W loads in flight
+        if (wl == 16) __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));
+        else if (wl == 8) __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
+        else if (wl == 4) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4));
+        else __builtin_amdgcn_s_waitcnt(0x0f70);
+#pragma unroll
+        for (int j = 0; j < SPW; j++)
+#pragma unroll
+            for (int t = 0; t < MT; t++)
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    asm volatile("" : "+v"(xv[j][t][i]));
+                    if (j >= nsw || 16 * t + row >= M) xv[j][t][i] = z;
+                }
+    }
     const char* ldsc = reinterpret_cast<const char*>(lds) + wave * 2 * SLOT;
     int slot = 0;
     for (int b = b0; b < nblk; b += bs, slot ^= 1) {
