@@ -130,7 +130,7 @@ struct Engine {
     std::map<std::string, int> tuned;
     Buf embed, head, norm, cos, sin;
     std::vector<Layer> layers;
-    Buf x, h, qkv, q, k, v, o, mlp, last, logits, tok, pos, slot, idx, table, lens, starts, next;
+    Buf x, h, ss, qkv, q, k, v, o, mlp, last, logits, tok, pos, slot, idx, table, lens, starts, next;
     // One device arena for a step's inputs, filled by one upload: for a step
     // of t (padded) rows, tok, pos, slot, idx, starts, lens (t ints each),
     // then table (t max_seq_pages ints). layout(t) points the buffers there;
@@ -277,6 +277,7 @@ struct Engine {
         size_t gd = (size_t)cfg.kv_heads * cfg.head_dim;
         TRY(alloc(t * d * 4, x));
         TRY(alloc(t * d * 2, h));
+        TRY(alloc(t * ((d + 7) / 8) * 4, ss));
         TRY(alloc(t * qr * 2, qkv));
         TRY(alloc(t * hd * 2, q));
         TRY(alloc(t * gd * 2, k));
@@ -334,21 +335,52 @@ struct Engine {
                    &oproj_norm_k, "fused"));
         TRY(kernel("linear_residual_rmsnorm", {{T, f}, {dm, f}, {T, dm}, {dm}, {T, dm}}, {{"BC", bc}}, 4,
                    &down_norm_k, "fused"));
+        // Decode steps of up to 32 rows defer each rmsnorm into the projection
+        // that consumes it: the residual projections leave Y = f16(R Wn) and
+        // per-8-column sums of squares of R (fused/linear_residual_prenorm),
+        // and gate_up / the next layer's QKV scale their rows by 1 / rms
+        // (fused/gate_up_rs, fused/qkv_rs_rope_kv): no normalisation launch
+        // between the two, and no second pass over R.
+        const bool prenorm = !prefill && T <= 32;
+        const int64_t nb8 = (dm + 7) / 8;
+        int o_pre_k = -1, down_pre_k = -1, gu_rs_k = -1, qkv_rs_k = -1;
+        if (prenorm) {
+            TRY(kernel("linear_residual_prenorm", {{T, nh * hd}, {dm, nh * hd}, {T, dm}, {dm}, {T, dm}, {nb8, T}}, {}, 4,
+                       &o_pre_k, "fused"));
+            TRY(kernel("linear_residual_prenorm", {{T, f}, {dm, f}, {T, dm}, {dm}, {T, dm}, {nb8, T}}, {}, 4,
+                       &down_pre_k, "fused"));
+            TRY(kernel("gate_up_rs", {{T, dm}, {nb8, T}, {f, dm}, {f, dm}, {T, f}}, {}, 4, &gu_rs_k, "fused"));
+            TRY(kernel("qkv_rs_rope_kv",
+                       {{T, dm}, {w, dm}, {T, w}, {T}, {T}, {npos, hd / 2}, {npos, hd / 2}, {T, nh, hd}, {ns, ng, hd},
+                        {ns, ng, hd}, {T, ng, hd}, {T, ng, hd}, {nb8, T}},
+                       {}, 4, &qkv_rs_k, "fused"));
+        }
 
         TRY(launch(embed_k, {B(tok), B(embed), B(x)}));
         TRY(launch(norm_k, {B(x), B(layers[0].n1), B(h), EPS}));
         for (size_t li = 0; li < layers.size(); li++) {
             const Layer& L = layers[li];
-            TRY(launch(qkv_k, {B(h), B(L.wqkv), B(qkv), B(pos), B(slot), B(cos), B(sin), B(q), B(L.kc), B(L.vc), B(k),
-                               B(v)}));
+            if (prenorm && li > 0)
+                TRY(launch(qkv_rs_k, {B(h), B(L.wqkv), B(qkv), B(pos), B(slot), B(cos), B(sin), B(q), B(L.kc), B(L.vc),
+                                      B(k), B(v), B(ss), EPS}));
+            else
+                TRY(launch(qkv_k, {B(h), B(L.wqkv), B(qkv), B(pos), B(slot), B(cos), B(sin), B(q), B(L.kc), B(L.vc),
+                                   B(k), B(v)}));
             if (prefill) TRY(launch(att_k, {B(q), B(k), B(v), B(starts), B(o), SC}));
             else TRY(launch(att_k, {B(q), B(L.kc), B(L.vc), B(table), B(lens), B(o), SC}));
-            TRY(launch(oproj_norm_k, {B(o), B(L.wo), B(x), B(L.n2), B(h), EPS}));
-            TRY(launch(gu_k, {B(h), B(L.wg), B(L.wu), B(mlp)}));
-            if (li + 1 < layers.size())
-                TRY(launch(down_norm_k, {B(mlp), B(L.wd), B(x), B(layers[li + 1].n1), B(h), EPS}));
-            else
+            if (prenorm) {
+                TRY(launch(o_pre_k, {B(o), B(L.wo), B(x), B(L.n2), B(h), B(ss)}));
+                TRY(launch(gu_rs_k, {B(h), B(ss), B(L.wg), B(L.wu), B(mlp), EPS}));
+            } else {
+                TRY(launch(oproj_norm_k, {B(o), B(L.wo), B(x), B(L.n2), B(h), EPS}));
+                TRY(launch(gu_k, {B(h), B(L.wg), B(L.wu), B(mlp)}));
+            }
+            if (li + 1 < layers.size()) {
+                if (prenorm) TRY(launch(down_pre_k, {B(mlp), B(L.wd), B(x), B(layers[li + 1].n1), B(h), B(ss)}));
+                else TRY(launch(down_norm_k, {B(mlp), B(L.wd), B(x), B(layers[li + 1].n1), B(h), EPS}));
+            } else {
                 TRY(launch(down_k, {B(mlp), B(L.wd), B(x)}));
+            }
         }
         if (bw == 0) return 0;
         int fin_k, head_k;
@@ -533,7 +565,7 @@ int tsl_engine_free(int engine) {
     if (!e) return tsl_fail(TSL_ERR_ARG, "no such engine");
     tsl_sync();
     // (tok, pos, slot, idx, starts, lens and table are views into `in`.)
-    Buf* bufs[] = {&e->embed, &e->norm, &e->cos, &e->sin, &e->x, &e->h, &e->qkv, &e->q, &e->k, &e->v,
+    Buf* bufs[] = {&e->embed, &e->norm, &e->cos, &e->sin, &e->x, &e->h, &e->ss, &e->qkv, &e->q, &e->k, &e->v,
                    &e->o, &e->mlp, &e->last, &e->logits, &e->in, &e->next};
     if (e->head.p != e->embed.p) tsl_free(e->head.p);
     for (Buf* b : bufs)

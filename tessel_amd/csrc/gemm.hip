@@ -958,18 +958,77 @@ TSL_DEV void rope_row_store(const RopeEpi& ep, int m, int h, int i0, int half, i
 
 template <int MT>
 constexpr int sl_xdepth() { return MT <= 2 ? 2 : 1; }
-template <int EPI, int MT, bool SPLIT>
+// The rows' deferred RMS normalisation (fused/linear_residual_prenorm and its
+// consumers): the producer leaves Y = f16(R Wn) with R the updated residual
+// and ss[b][m] = the sum of R[m][n]^2 over its 8-column block b (column
+// order); a consumer takes rs[m] = 1 / sqrt(sum_b ss[b][m] / K + eps) (the
+// partial sums added in a fixed order) and scales its products of row m by
+// rs[m] before its epilogue: rmsnorm(R) Wn W^T = rs (R Wn) W^T.
+struct NormPre {
+    const u16* w = nullptr;  // producer: Wn [N]
+    u16* y = nullptr;        // producer: Y [M, N]
+    const float* ss = nullptr;  // consumer: [nr, M]
+    int nr = 0;
+    float eps = 0.0f;
+};
+
+// Thread t of a 512-thread workgroup: rs[m] into lds_rs[m] for m < M <= 32.
+// Thread (q = t / 32, m = t % 32) adds partials q, q + 16, .. in order
+// (loaded before the call, ssv), then m adds its 16 sums in q order.
+TSL_DEV void rs_from_partials(const float (&ssv)[16], int nr, int M, int K, float eps, float* lds_sum,
+                              float* lds_rs) {
+    const int t = threadIdx.x, q = t >> 5;
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) a += q + 16 * i < nr ? ssv[i] : 0.0f;
+    lds_sum[t] = a;
+    __syncthreads();
+    if (t < M) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int qq = 0; qq < 16; qq++) tot += lds_sum[qq * 32 + t];
+        lds_rs[t] = 1.0f / sqrtf(tot / (float)K + eps);
+    }
+    __syncthreads();
+}
+// The partial sums thread t adds (nr <= 256), written out as loads the
+// compiler does not count (issued before the caller's W loads; the caller
+// waits for them with an explicit vmcnt, then fences them with
+// ssv_fence).
+TSL_DEV void ssv_load(const float* ss, int nr, int M, float (&ssv)[16]) {
+    const int t = threadIdx.x, m = min(t & 31, M - 1), q = t >> 5;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int b = min(q + 16 * i, nr - 1);
+        asm volatile("global_load_dword %0, %1, off" : "=v"(ssv[i]) : "v"(ss + (size_t)b * M + m));
+    }
+}
+TSL_DEV void ssv_fence(float (&ssv)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) asm volatile("" : "+v"(ssv[i]));
+}
+
+// R8 (linear_residual_prenorm, EPI_RESID): blocks of 8 rows of W over the
+// whole K (up to 2 SL_KS, the same LDS); after R += Y the block writes
+// np.y = f16(R np.w) for its 8 columns and the per-row sums of squares of
+// the new R to part[block][m] (column order). RS (a consumer, ROPE): the
+// sums of row m are scaled by rs[m] from np.ss first.
+template <int EPI, int MT, bool SPLIT, bool R8 = false, bool RS = false>
 __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __restrict__ X, const u16* __restrict__ W,
                                                                    const u16* __restrict__ W2, void* C,
                                                                    const u16* __restrict__ bias, int M, int N, int K,
-                                                                   float* __restrict__ part, RopeEpi ep) {
+                                                                   float* __restrict__ part, RopeEpi ep,
+                                                                   NormPre np = {}) {
     constexpr bool ROPE = EPI == EPI_ROPE;
     constexpr bool DUAL = EPI == EPI_SWIGLU || ROPE;  // paired rows: 8 + 8 per block
     static_assert(!(ROPE && SPLIT), "the rotary epilogue needs whole sums");
-    constexpr int WB = 16 * SL_KS * 2;           // LDS bytes of the W block
+    static_assert(!R8 || (EPI == EPI_RESID && !SPLIT), "8-row blocks: the residual epilogue over the whole K");
+    static_assert(!RS || (ROPE && MT <= 2), "row scaling: the rotary consumer, M <= 32");
+    constexpr int KSL = R8 ? 2 * SL_KS : SL_KS;  // k values per block (slice), at most
+    constexpr int WB = (R8 ? 8 : 16) * KSL * 2;  // LDS bytes of the W block
     constexpr int XS = 16 * MT * 128;            // LDS bytes of one X step
     constexpr int XD = sl_xdepth<MT>();          // X stages per wavefront
-    constexpr int MAXU = (SL_KS / 64 + SK_WAVES - 1) / SK_WAVES;  // k steps per wavefront, at most
+    constexpr int MAXU = (KSL / 64 + SK_WAVES - 1) / SK_WAVES;  // k steps per wavefront, at most
     constexpr int XL = 2 * MT;                   // X loads per step (8 rows each)
     __shared__ __attribute__((aligned(16))) u16 lds[(WB + SK_WAVES * XD * XS) / 2];
     __shared__ __attribute__((aligned(16))) float red[SK_WAVES][4][64];
@@ -977,7 +1036,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row = lane & 15, g = lane >> 4;
     // Rows of this block: n0 .. n0 + 15 of W, or n0 .. n0 + 7 of Wg and of Wu.
-    const int n0 = blockIdx.x * (DUAL ? 8 : 16);
+    const int n0 = blockIdx.x * (DUAL || R8 ? 8 : 16);
     const int nb = K / 128, S = SPLIT ? gridDim.y : 1, ks = SPLIT ? blockIdx.y : 0;
     const int b0 = ks * nb / S, b1 = (ks + 1) * nb / S;
     const int k0 = 128 * b0, KS = 128 * (b1 - b0), cpr = KS / 8, nst = KS / 64;
@@ -996,16 +1055,19 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         if (tid < 2 * M) rslot = ep.slot[tid >> 1];  // the write-out's row
     }
 
-    // W block: 16 cpr chunks; load q covers linear chunks 64 q .. 64 q + 63
-    // (row p / cpr, position p % cpr). Rows past N read as zero.
+    // The consumer's partial sums of squares, before any W load.
+    float ssv[RS ? 16 : 1];
+    if constexpr (RS) ssv_load(np.ss, np.nr, M, ssv);
+    // W block: 16 cpr chunks (R8: 8 cpr); load q covers linear chunks 64 q ..
+    // 64 q + 63 (row p / cpr, position p % cpr). Rows past N read as zero.
     {
-        const int rows = min(DUAL ? 8 : 16, N - n0);
+        const int rows = min(DUAL || R8 ? 8 : 16, N - n0);
         const uint32_t range = (uint32_t)(((long)(rows - 1) * K + KS) * 2);
         // First rows of the block's two halves (rotary pairs: within one head of W).
         const long ra = ROPE ? (long)(n0 / ep.D2) * ep.D + n0 % ep.D2 : n0;
         const i32x4 rw = make_rsrc(W + ra * K + k0, range);
         const i32x4 rw2 = make_rsrc(ROPE ? W + (ra + ep.D2) * K + k0 : (DUAL ? W2 : W) + (size_t)n0 * K + k0, range);
-        const int nq = cpr / 4;
+        const int nq = (R8 ? 8 : 16) * cpr / 64;
         for (int q = wave; q < nq; q += SK_WAVES) {
             const int p = 64 * q + lane, r = p / cpr, pos = p - r * cpr;
             const int rr = DUAL ? r & 7 : r;  // row within its matrix
@@ -1043,7 +1105,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
 #pragma unroll
     for (int t = 0; t < MT; t++) acc[t] = float4v{};
     const char* ldsc = reinterpret_cast<const char*>(lds);
-    const char* wrow = ldsc + row * KS * 2;
+    const char* wrow = ldsc + (R8 ? row & 7 : row) * KS * 2;  // (R8: rows 8..15 repeat 0..7, sums dropped)
     const char* xbase = ldsc + WB + wave * XD * XS;
 #pragma unroll
     for (int u = 0; u < MAXU; u++) {
@@ -1110,6 +1172,20 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
             up[t] = tid < 256 && l < 32 ? red[0][r][l + 32] : 0.0f;
         }
     }
+    if constexpr (RS) {
+        // rs[m] (the ring is free: every wavefront is past the reduction's
+        // barriers), then the sums of row m scaled by it.
+        ssv_fence(ssv);
+        float* rsb = reinterpret_cast<float*>(lds + WB / 2);  // [512] sums, then [32] rs
+        rs_from_partials(ssv, np.nr, M, K, np.eps, rsb, rsb + 512);
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int m = 16 * t + (l & 15);
+            const float f = m < M ? rsb[512 + m] : 0.0f;
+            sum[t] *= f;
+            up[t] *= f;
+        }
+    }
     if constexpr (ROPE) {
         // The block's 8 pairs lie in one head (D2 % 8 == 0): the rotated
         // halves go through LDS, then each token row leaves as two 16-byte
@@ -1132,6 +1208,41 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         const int h = n0 / ep.D2, i0 = n0 % ep.D2;
         if (tid < 2 * M)  // M <= 64: one row half per thread
             rope_row_store(ep, tid >> 1, h, i0, tid & 1, rslot, *reinterpret_cast<const u32x4*>(&yb[tid >> 1][8 * (tid & 1)]));
+        return;
+    }
+    if constexpr (R8) {
+        // R += Y for the block's 8 columns; np.y = f16(R np.w); then the
+        // squares of the new values summed per row in column order (through
+        // red, now free).
+        float* sq = &red[0][0][0];  // [MT][8 columns][16 rows]
+        static_assert(MT * 8 * 16 <= SK_WAVES * 4 * 64, "squares fit the reduction buffer");
+        __syncthreads();  // every wavefront has read red
+        if (tid < 256 && l < 32) {
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int j = 4 * (l >> 4) + r, n = n0 + j, m = 16 * t + (l & 15);
+                float nv = 0.0f;
+                if (m < M && n < N) {
+                    float* o = reinterpret_cast<float*>(C) + (size_t)m * N + n;
+                    nv = *o + sum[t];
+                    *o = nv;
+                    float yv = nv * h2f(np.w[n]);
+                    asm volatile("" : "+v"(yv));  // rounded to f32, then to f16 (no fused multiply-convert)
+                    np.y[(size_t)m * N + n] = f2h(yv);
+                }
+                sq[(t * 8 + j) * 16 + (l & 15)] = nv * nv;
+            }
+        }
+        __syncthreads();
+        if (tid < 16 * MT) {
+            const int t = tid >> 4, mm = tid & 15, m = 16 * t + mm;
+            if (m < M) {
+                float a = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) a += sq[(t * 8 + j) * 16 + mm];
+                part[(size_t)blockIdx.x * M + m] = a;
+            }
+        }
         return;
     }
     if constexpr (DUAL) {
@@ -1161,10 +1272,14 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
 // lines, 2 rows per 1 KB direct-to-LDS load) into its own 2-slot LDS ring,
 // the next block's loads in flight while it computes. Block layout, MFMA,
 // reduction and epilogue are gemm_skinny_lds's (M <= 32).
-template <int EPI, int MT>
+//
+// RS (a consumer of linear_residual_prenorm): the sums of row m are scaled by
+// rs[m] from np.ss before the epilogue.
+template <int EPI, int MT, bool RS = false>
 __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __restrict__ X, const u16* __restrict__ W,
                                                                    const u16* __restrict__ W2, void* C,
-                                                                   const u16* __restrict__ bias, int M, int N, int K) {
+                                                                   const u16* __restrict__ bias, int M, int N, int K,
+                                                                   NormPre np = {}) {
     constexpr bool DUAL = EPI == EPI_SWIGLU;
     constexpr int SPW = 4;                   // most k steps per wavefront (K <= 2048)
     constexpr int SLOT = 16 * SPW * 128;     // LDS bytes of one block's segments
@@ -1189,6 +1304,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
     // W loads in flight, and each operand passes through an empty asm after
     // it, so nothing reads it earlier.
     const u32x4 z = {0, 0, 0, 0};
+    float ssv[RS ? 16 : 1];
+    if constexpr (RS) ssv_load(np.ss, np.nr, M, ssv);
     u32x4 xv[SPW][MT][2];
 #pragma unroll
     for (int j = 0; j < SPW; j++)
@@ -1238,6 +1355,15 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
                     asm volatile("" : "+v"(xv[j][t][i]));
                     if (j >= nsw || 16 * t + row >= M) xv[j][t][i] = z;
                 }
+    }
+    float rsv[MT];  // rs of rows 16 t + row (RS)
+    if constexpr (RS) {
+        ssv_fence(ssv);
+        float* rsb = &red[0][0][0];
+        rs_from_partials(ssv, np.nr, M, K, np.eps, rsb, rsb + 512);
+#pragma unroll
+        for (int t = 0; t < MT; t++) rsv[t] = 16 * t + row < M ? rsb[512 + 16 * t + row] : 0.0f;
+        __syncthreads();  // red is the reduction's again
     }
     const char* ldsc = reinterpret_cast<const char*>(lds) + wave * 2 * SLOT;
     int slot = 0;
@@ -1299,7 +1425,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
             for (int t = 0; t < MT; t++) {
                 const int n = n0 + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
                 if (m >= M || n >= N) continue;
-                sk_store<EPI>(C, bias, N, m, n, sum[t], DUAL ? up[t] : 0.0f);
+                if constexpr (RS) sk_store<EPI>(C, bias, N, m, n, sum[t] * rsv[t], DUAL ? up[t] * rsv[t] : 0.0f);
+                else sk_store<EPI>(C, bias, N, m, n, sum[t], DUAL ? up[t] : 0.0f);
             }
         }
         // The block after next into the slot just read. Issued after the
@@ -1619,7 +1746,10 @@ int launch_linear_residual_rmsnorm(TslKernel& k, const uint64_t* a, hipStream_t 
 // epilogue rotates and stores (QKV is then left unwritten); the outputs are
 // the bits the three launches give. Other shapes launch the three.
 int launch_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s);
-int launch_qkv_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
+namespace {
+// fused/qkv_rope_kv with X given (a[0] is not read), and with np.ss set the
+// rows of X scaled by rs (fused/qkv_rs_rope_kv; T <= 32 on the fused path).
+int qkv_rope_kv_run(TslKernel& k, const uint64_t* a, hipStream_t s, const u16* X, float* part, const NormPre& np) {
     const int T = k.dim("T"), W = k.dim("W"), Dm = k.dim("Dm");
     RopeEpi ep;
     ep.H = k.dim("H"), ep.G = k.dim("G"), ep.D = k.dim("D"), ep.D2 = k.dim("D2"), ep.NS = k.dim("NS");
@@ -1628,8 +1758,8 @@ int launch_qkv_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
     const bool fused = p.use && p.lds && p.split == 1 && ep.D == 2 * ep.D2 && ep.D2 % 8 == 0 &&
                        W == (ep.H + 2 * ep.G) * ep.D;
     if (!fused) {
-        if (int e = gemm_dispatch<true, EPI_F16>(P<u16>(a[0]), P<u16>(a[1]), nullptr, P<void>(a[2]), nullptr, T, W, Dm,
-                                                 s, "qkv_rope_kv", reinterpret_cast<float*>(k.scratch)))
+        if (int e = gemm_dispatch<true, EPI_F16>(X, P<u16>(a[1]), nullptr, P<void>(a[2]), nullptr, T, W, Dm, s,
+                                                 "qkv_rope_kv", part))
             return e;
         return launch_rope_kv(k, a + 2, s);
     }
@@ -1637,7 +1767,16 @@ int launch_qkv_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
     ep.Q = P<u16>(a[7]), ep.Kc = P<u16>(a[8]), ep.Vc = P<u16>(a[9]), ep.K = P<u16>(a[10]), ep.V = P<u16>(a[11]);
     const int pairs = W / 2;
     const unsigned blocks = (pairs + 7) / 8;
-    const u16 *X = P<u16>(a[0]), *Wq = P<u16>(a[1]);
+    const u16* Wq = P<u16>(a[1]);
+    if (np.ss) {  // T <= 32
+        if (T <= 16)
+            hipLaunchKernelGGL((gemm_skinny_lds<EPI_ROPE, 1, false, false, true>), dim3(blocks), dim3(64 * SK_WAVES), 0,
+                               s, X, Wq, nullptr, nullptr, nullptr, T, pairs, Dm, nullptr, ep, np);
+        else
+            hipLaunchKernelGGL((gemm_skinny_lds<EPI_ROPE, 2, false, false, true>), dim3(blocks), dim3(64 * SK_WAVES), 0,
+                               s, X, Wq, nullptr, nullptr, nullptr, T, pairs, Dm, nullptr, ep, np);
+        return TSL_LAUNCHED("qkv_rs_rope_kv");
+    }
     auto go = [&](auto mt) {
         hipLaunchKernelGGL((gemm_skinny_lds<EPI_ROPE, decltype(mt)::value, false>), dim3(blocks), dim3(64 * SK_WAVES), 0,
                            s, X, Wq, nullptr, nullptr, nullptr, T, pairs, Dm, nullptr, ep);
@@ -1649,6 +1788,159 @@ int launch_qkv_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
         default: go(std::integral_constant<int, 4>{}); break;
     }
     return TSL_LAUNCHED("qkv_rope_kv");
+}
+
+// Whether the qkv product takes the fused skinny path (as qkv_rope_kv_run decides).
+bool qkv_fused(TslKernel& k) {
+    const int T = k.dim("T"), W = k.dim("W"), Dm = k.dim("Dm"), D = k.dim("D"), D2 = k.dim("D2");
+    const SkPlan p = sk_plan(true, T, W, Dm);
+    return p.use && p.lds && p.split == 1 && D == 2 * D2 && D2 % 8 == 0 && W == (k.dim("H") + 2 * k.dim("G")) * D;
+}
+
+// The fallback of the rs consumers: H[m] = f16(Y[m] rs[m]), rs from the
+// partial sums in the consumers' order (16 strided sums, then those in order).
+__global__ __launch_bounds__(256) void rows_rs_kernel(const u16* __restrict__ Y, const float* __restrict__ SS,
+                                                      u16* __restrict__ H, int M, int K, int NB, float eps) {
+    __shared__ float pr[16];
+    const int m = blockIdx.x, t = threadIdx.x;
+    if (t < 16) {
+        float a = 0.0f;
+        for (int b = t; b < NB; b += 16) a += SS[(size_t)b * M + m];
+        pr[t] = a;
+    }
+    __syncthreads();
+    float a = 0.0f;
+    for (int q = 0; q < 16; q++) a += pr[q];
+    const float rs = 1.0f / sqrtf(a / (float)K + eps);
+    for (int k = t; k < K; k += 256) H[(size_t)m * K + k] = f2h(h2f(Y[(size_t)m * K + k]) * rs);
+}
+
+// The prenorm producer's fallback: Y = f16(R Wn) and the per-8-column sums
+// of squares, as the fused kernel computes them.
+__global__ __launch_bounds__(256) void prenorm_kernel(const float* __restrict__ R, const u16* __restrict__ Wn,
+                                                      u16* __restrict__ Y, float* __restrict__ SS, int M, int N,
+                                                      int NB) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)NB * M) return;
+    const int b = (int)(i / M), m = (int)(i % M);
+    float a = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        const int n = 8 * b + j;
+        if (n >= N) break;
+        const float v = R[(size_t)m * N + n];
+        float yv = v * h2f(Wn[n]);
+        asm volatile("" : "+v"(yv));  // rounded to f32, then to f16 (as the fused kernel)
+        Y[(size_t)m * N + n] = f2h(yv);
+        float q = v * v;
+        asm volatile("" : "+v"(q));  // the product rounded, not contracted into an fma (as in the fused kernel)
+        a += q;
+    }
+    SS[i] = a;
+}
+}  // namespace
+
+int launch_qkv_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    return qkv_rope_kv_run(k, a, s, P<u16>(a[0]), reinterpret_cast<float*>(k.scratch), NormPre{});
+}
+
+// fused/linear_residual_prenorm (the engine's fusion, not a .tl kernel):
+// llm/linear_residual, R += X W^T, leaving for the next projection's rmsnorm
+// Y = f16(R Wn) and SS[b][m], the sum over the 8 columns n = 8 b .. 8 b + 7
+// (column order) of the new R[m][n]^2. Arguments X [M, K], W [N, K], R [M, N],
+// Wn [N], Y [M, N], SS [NB, M], NB = ceil(N / 8).
+int launch_linear_residual_prenorm(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    const int M = k.dim("M"), N = k.dim("N"), K = k.dim("K"), NB = k.dim("NB");
+    if (NB != (N + 7) / 8) return tsl_fail(-2, "linear_residual_prenorm: NB must be ceil(N / 8)");
+    if (M == 0 || N == 0) return 0;
+    const u16 *X = P<u16>(a[0]), *W = P<u16>(a[1]);
+    float* R = P<float>(a[2]);
+    NormPre np;
+    np.w = P<u16>(a[3]), np.y = P<u16>(a[4]);
+    float* SS = P<float>(a[5]);
+    if (M <= 64 && K % 128 == 0 && K > 0 && K <= 2 * SL_KS) {
+        auto go = [&](auto mt) {
+            hipLaunchKernelGGL((gemm_skinny_lds<EPI_RESID, decltype(mt)::value, false, true>), dim3(NB),
+                               dim3(64 * SK_WAVES), 0, s, X, W, nullptr, R, nullptr, M, N, K, SS, RopeEpi{}, np);
+        };
+        switch ((M + 15) / 16) {
+            case 1: go(std::integral_constant<int, 1>{}); break;
+            case 2: go(std::integral_constant<int, 2>{}); break;
+            case 3: go(std::integral_constant<int, 3>{}); break;
+            default: go(std::integral_constant<int, 4>{}); break;
+        }
+        return TSL_LAUNCHED("linear_residual_prenorm");
+    }
+    if (int e = gemm_dispatch<true, EPI_RESID>(X, W, nullptr, R, nullptr, M, N, K, s, "linear_residual_prenorm", nullptr))
+        return e;
+    const long n = (long)NB * M;
+    hipLaunchKernelGGL(prenorm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, R, np.w, np.y, SS, M, N, NB);
+    return TSL_LAUNCHED("linear_residual_prenorm");
+}
+
+// fused/gate_up_rs (the engine's fusion, not a .tl kernel): llm/gate_up of
+// rmsnorm(R) Wn given as Y = f16(R Wn) and SS (linear_residual_prenorm):
+// each row's products are scaled by rs = 1 / sqrt(sum SS / K + eps).
+// Arguments Y [M, K], SS [NB, M], Wg [F, K], Wu [F, K], O [M, F], eps.
+bool rs_pst_fits(int M, int F, int K, int NB) {
+    return M <= 32 && (K == 1024 || K == 2048) && NB <= 256 && (F + 7) / 8 > num_cus();
+}
+int launch_gate_up_rs(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    const int M = k.dim("M"), F = k.dim("F"), K = k.dim("K"), NB = k.dim("NB");
+    if (M == 0 || F == 0) return 0;
+    NormPre np;
+    np.ss = P<float>(a[1]), np.nr = NB, np.eps = arg_f32(a[5]);
+    const u16 *Y = P<u16>(a[0]), *Wg = P<u16>(a[2]), *Wu = P<u16>(a[3]);
+    u16* O = P<u16>(a[4]);
+    if (rs_pst_fits(M, F, K, NB)) {
+        if (M <= 16)
+            hipLaunchKernelGGL((gemm_skinny_pst<EPI_SWIGLU, 1, true>), dim3(num_cus()), dim3(64 * SK_WAVES), 0, s, Y, Wg,
+                               Wu, O, nullptr, M, F, K, np);
+        else
+            hipLaunchKernelGGL((gemm_skinny_pst<EPI_SWIGLU, 2, true>), dim3(num_cus()), dim3(64 * SK_WAVES), 0, s, Y, Wg,
+                               Wu, O, nullptr, M, F, K, np);
+        return TSL_LAUNCHED("gate_up_rs");
+    }
+    if (!k.scratch) return tsl_fail(-1, "gate_up_rs: no scratch for the scaled rows");
+    u16* H = reinterpret_cast<u16*>(k.scratch);
+    hipLaunchKernelGGL(rows_rs_kernel, dim3(M), dim3(256), 0, s, Y, np.ss, H, M, K, NB, np.eps);
+    if (int e = TSL_LAUNCHED("gate_up_rs")) return e;
+    return gemm_dispatch<true, EPI_SWIGLU>(H, Wg, Wu, O, nullptr, M, F, K, s, "gate_up_rs", nullptr);
+}
+int prepare_gate_up_rs(TslKernel& k) {
+    const int64_t M = k.dim("M"), F = k.dim("F"), K = k.dim("K"), NB = k.dim("NB");
+    if (NB < 1) return tsl_fail(-2, "gate_up_rs: NB must be at least 1");
+    if (M > (1 << 20) || K > (1 << 20) || rs_pst_fits((int)M, (int)F, (int)K, (int)NB)) return 0;
+    const size_t bytes = (size_t)M * K * 2;
+    if (bytes == 0) return 0;
+    if (tsl_hip_check(hipMalloc(&k.scratch, bytes), "gate_up_rs scratch")) return -1;
+    k.scratch_bytes = bytes;
+    return 0;
+}
+
+// fused/qkv_rs_rope_kv (the engine's fusion, not a .tl kernel):
+// fused/qkv_rope_kv of rmsnorm(R) Wn given as Y = f16(R Wn) and SS
+// (linear_residual_prenorm), its arguments then SS [NB, T], eps.
+bool qkv_rs_fits(TslKernel& k) { return k.dim("T") <= 32 && k.dim("NB") <= 256 && qkv_fused(k); }
+int launch_qkv_rs_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
+    const int T = k.dim("T"), Dm = k.dim("Dm"), NB = k.dim("NB");
+    if (T == 0) return 0;
+    NormPre np;
+    np.ss = P<float>(a[12]), np.nr = NB, np.eps = arg_f32(a[13]);
+    if (qkv_rs_fits(k)) return qkv_rope_kv_run(k, a, s, P<u16>(a[0]), nullptr, np);
+    if (!k.scratch) return tsl_fail(-1, "qkv_rs_rope_kv: no scratch for the scaled rows");
+    u16* H = reinterpret_cast<u16*>(k.scratch);
+    hipLaunchKernelGGL(rows_rs_kernel, dim3(T), dim3(256), 0, s, P<u16>(a[0]), np.ss, H, T, Dm, NB, np.eps);
+    if (int e = TSL_LAUNCHED("qkv_rs_rope_kv")) return e;
+    return qkv_rope_kv_run(k, a, s, H, nullptr, NormPre{});
+}
+int prepare_qkv_rs_rope_kv(TslKernel& k) {
+    if (k.dim("NB") < 1) return tsl_fail(-2, "qkv_rs_rope_kv: NB must be at least 1");
+    if (qkv_rs_fits(k)) return 0;
+    const size_t bytes = (size_t)k.dim("T") * k.dim("Dm") * 2;
+    if (bytes == 0) return 0;
+    if (tsl_hip_check(hipMalloc(&k.scratch, bytes), "qkv_rs_rope_kv scratch")) return -1;
+    k.scratch_bytes = bytes;
+    return 0;
 }
 
 // Sizes the split-K partials (the skinny path at decode-sized M, the 128 x 128

@@ -44,6 +44,11 @@ int launch_kv_write(TslKernel&, const uint64_t*, hipStream_t);
 int launch_rope_kv(TslKernel&, const uint64_t*, hipStream_t);
 int launch_linear_residual_rmsnorm(TslKernel&, const uint64_t*, hipStream_t);
 int launch_qkv_rope_kv(TslKernel&, const uint64_t*, hipStream_t);
+int launch_linear_residual_prenorm(TslKernel&, const uint64_t*, hipStream_t);
+int launch_gate_up_rs(TslKernel&, const uint64_t*, hipStream_t);
+int launch_qkv_rs_rope_kv(TslKernel&, const uint64_t*, hipStream_t);
+int prepare_gate_up_rs(TslKernel&);
+int prepare_qkv_rs_rope_kv(TslKernel&);
 int launch_argmax(TslKernel&, const uint64_t*, hipStream_t);
 int launch_flash_attention(TslKernel&, const uint64_t*, hipStream_t);
 int launch_prefill_attention(TslKernel&, const uint64_t*, hipStream_t);
@@ -147,6 +152,24 @@ std::vector<KernelDef> g_defs = {
     // Not a .tl kernel: argmax of each row (src/llm/mod.rs:132-140), so the
     // scheduler reads back token ids instead of logits.
     {"fused", "argmax", "X: f32[B, V], T: i32[B]", "", "", launch_argmax, nullptr},
+    // Not a .tl kernel: llm/linear_residual that leaves the next rmsnorm
+    // deferred, as Y = f16(R Wn) and per-8-column sums of squares of R (the
+    // engine's fusion; its consumers are gate_up_rs and qkv_rs_rope_kv).
+    {"fused", "linear_residual_prenorm",
+     "X: f16[M, K], W: f16[N, K], R: f32[M, N], Wn: f16[N], Y: f16[M, N], SS: f32[NB, M]", "", "",
+     launch_linear_residual_prenorm, nullptr},
+    // Not a .tl kernel: llm/gate_up of rmsnorm(R) Wn given as Y and SS (the
+    // engine's fusion).
+    {"fused", "gate_up_rs",
+     "Y: f16[M, K], SS: f32[NB, M], Wg: f16[F, K], Wu: f16[F, K], O: f16[M, F], eps: f32", "", "",
+     launch_gate_up_rs, prepare_gate_up_rs},
+    // Not a .tl kernel: fused/qkv_rope_kv of rmsnorm(R) Wn given as X = Y and
+    // SS (the engine's fusion; qkv_rope_kv's arguments, then SS and eps).
+    {"fused", "qkv_rs_rope_kv",
+     "X: f16[T, Dm], Wqkv: f16[W, Dm], QKV: f16[T, W], pos: i32[T], slot: i32[T], C: f32[NPOS, D2], "
+     "S: f32[NPOS, D2], Q: f16[T, H, D], Kc: f16[NS, G, D], Vc: f16[NS, G, D], K: f16[T, G, D], V: f16[T, G, D], "
+     "SS: f32[NB, T], eps: f32",
+     "", "D2 D", launch_qkv_rs_rope_kv, prepare_qkv_rs_rope_kv},
     {"llm", "prefill_attention",
      "Q: f16[S, H, D], K: f16[S, G, D], V: f16[S, G, D], starts: i32[S], O: f16[S, H, D], scale: f32",
      "BM = 64, BN = 64", "D", launch_prefill_attention, prepare_attention},

@@ -609,6 +609,97 @@ def test_fused_qkv_rope_kv(cfgname, t):
     parity("fused Q", got[7], oracle.rope_q(oracle.llm_linear(x, wq), pos, c, s, H, D))
 
 
+def _ss_ref(r):
+    """SS[b][m]: the squares of R[m][8 b .. 8 b + 7] added in column order in f32."""
+    m, n = r.shape
+    nb = (n + 7) // 8
+    pad = np.zeros((m, nb * 8), np.float32)
+    pad[:, :n] = r
+    sq = (pad * pad).reshape(m, nb, 8)
+    acc = np.zeros((m, nb), np.float32)
+    for j in range(8):
+        acc = (acc + sq[:, :, j]).astype(np.float32)
+    return np.ascontiguousarray(acc.T)
+
+
+def _prenorm(r, m, ko, dm):
+    """fused/linear_residual_prenorm on seeded inputs, checked: R against the
+    oracle, Y = f16(R Wn) and the sums of squares bit-exact against their
+    definitions from the returned R. Returns (Y, SS, the oracle's R, Wn)."""
+    x = r.tensor("f16", [m, ko], 1.0)
+    w = r.tensor("f16", [dm, ko], 1.0 / np.sqrt(ko))
+    res = r.tensor("f32", [m, dm], 1.0)
+    wn = r.tensor("f16", [dm], 1.0)
+    nb = (dm + 7) // 8
+    out = T.run("fused", "linear_residual_prenorm",
+                [x, w, res.copy(), wn, np.zeros((m, dm), np.float16), np.zeros((nb, m), np.float32)], outputs=[2, 4, 5])
+    want_r = oracle.linear_residual(x, w, res.copy())
+    parity("prenorm R", out[2], want_r)
+    y_def = (out[2].astype(np.float32) * wn.astype(np.float32)).astype(np.float16)
+    np.testing.assert_array_equal(out[4].view(np.uint16), y_def.view(np.uint16))
+    np.testing.assert_array_equal(out[5].view(np.uint32), _ss_ref(out[2]).view(np.uint32))
+    return out[4], out[5], want_r, wn
+
+
+@pytest.mark.parametrize("m,ko,dm,f", [(32, 2048, 2048, 5632), (17, 5632, 2048, 5632), (9, 1024, 1024, 4000),
+                                       (40, 2048, 2048, 5632), (100, 192, 100, 300)])
+def test_fused_prenorm_then_gate_up_rs(m, ko, dm, f):
+    # The engine's decode-step pair for the MLP input: the o projection leaves
+    # Y = f16(R Wn) and per-8-column sums of squares (linear_residual_prenorm),
+    # and gate_up_rs scales each row's products by 1 / rms(R): against the
+    # oracle's linear_residual -> rmsnorm -> gate_up. M <= 32 with K = 1024 or
+    # 2048 and F / 8 > the CUs take the fused kernels; the others the fallbacks.
+    # Two launches of the pair agree bit for bit.
+    _say("fused prenorm + gate_up_rs", m, ko, dm, f)
+    r = oracle.Rng(810 + m + f)
+    y, ss, want_r, wn = _prenorm(r, m, ko, dm)
+    wg = r.tensor("f16", [f, dm], 1.0 / np.sqrt(dm))
+    wu = r.tensor("f16", [f, dm], 1.0 / np.sqrt(dm))
+    eps = [T.F32(1e-5)]
+    got = [T.run("fused", "gate_up_rs", [y, ss, wg, wu, np.zeros((m, f), np.float16)], eps, outputs=[4])[4]
+           for _ in range(2)]
+    np.testing.assert_array_equal(got[0].view(np.uint16), got[1].view(np.uint16))
+    bc = 1 << (dm - 1).bit_length()
+    h = oracle.rmsnorm(want_r.astype(np.float32), wn, 1e-5, BC=bc)
+    parity("gate_up_rs", got[0], oracle.gate_up(h, wg, wu))
+
+
+@pytest.mark.parametrize("cfgname,t", [("tinyllama", 32), ("tinyllama", 7), ("tinyllama", 40), ("tiny", 16)])
+def test_fused_prenorm_then_qkv_rs_rope_kv(cfgname, t):
+    # The engine's decode-step pair for the next layer's attention input: the
+    # down projection leaves Y = f16(R Wn) and the sums of squares, and
+    # qkv_rs_rope_kv scales each row's QKV sums by 1 / rms(R) before the
+    # f16 rounding, the rotation and the cache write: against qkv_rope_kv of
+    # the oracle's rmsnorm(R) (within the float tolerance; slots and positions
+    # outside the tables included). t = 40 and the tiny config take the
+    # fallbacks.
+    _say("fused prenorm + qkv_rs_rope_kv", cfgname, t)
+    cfg = getattr(oracle.Config, cfgname)()
+    c, s = oracle.rope_tables(cfg)
+    H, G, D, dm, W = cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.dim, cfg.qkv()
+    r = oracle.Rng(31 + t)
+    y, ss, want_r, wn = _prenorm(r, t, cfg.ffn, dm)
+    wq = r.tensor("f16", [W, dm], 1.0 / np.sqrt(dm))
+    pos = np.array([(i * 97) % cfg.max_pos for i in range(t)], np.int32)
+    pos[0] = cfg.max_pos + 5
+    NS = 3 * t + 7
+    slot = np.array([(i * 7) % NS for i in range(t)], np.int32)
+    slot[-1] = NS
+    slot[-2] = -1
+    Kc = r.tensor("f16", [NS, G, D])
+    Vc = r.tensor("f16", [NS, G, D])
+    z = lambda *sh: np.zeros(sh, np.float16)
+    got = T.run("fused", "qkv_rs_rope_kv",
+                [y, wq, z(t, W), pos, slot, c, s, z(t, H, D), Kc.copy(), Vc.copy(), z(t, G, D), z(t, G, D), ss],
+                [T.F32(cfg.eps)])
+    bc = 1 << (dm - 1).bit_length()
+    h = oracle.rmsnorm(want_r.astype(np.float32), wn, cfg.eps, BC=bc)
+    want = T.run("fused", "qkv_rope_kv", [h, wq, z(t, W), pos, slot, c, s, z(t, H, D), Kc.copy(), Vc.copy(),
+                                          z(t, G, D), z(t, G, D)])
+    for i, name in ((7, "Q"), (8, "Kc"), (9, "Vc"), (10, "K"), (11, "V")):
+        parity(f"qkv_rs {name}", got[i], want[i])
+
+
 @pytest.mark.parametrize("cfgname", ["tiny", "tinyllama"])
 def test_rope_and_kv_write(cfgname):
     _say("rope/kv_write", cfgname)
