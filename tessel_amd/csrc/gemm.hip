@@ -557,15 +557,17 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         }
 }
 
-// The 256 x 256 tile for large products (K % 64 == 0), as a ping-pong of
-// two wavefront groups. 8 wavefronts of 128 x 64 (WGM 2 x WGN 4, as
-// gemm_big's 256 x 256); group 0 (waves 0-3) and group 1 (waves 4-7) put one
-// wavefront on each SIMD and take turns, separated by workgroup barriers:
-// while one group runs a K step's 32 MFMAs back to back from registers, the
-// other reads its next K step's operands from LDS into registers. Group 0
-// also loads the A tile of the next step and group 1 the B tile of the step
-// after that, so the direct-to-LDS writes are spread over both groups'
-// read phases. LDS is gemm_big's 2-stage layout and swizzle.
+// Large products as a ping-pong of two wavefront groups (K % (64 NH) == 0).
+// 8 wavefronts of (BM/2) x (BN/4) (256 x 256: 128 x 64, as gemm_big's); group
+// 0 (waves 0-3) and group 1 (waves 4-7) put one wavefront on each SIMD and
+// take turns, separated by workgroup barriers: while one group runs a
+// phase's MFMAs back to back from registers, the other reads its next
+// phase's operands from LDS into registers. A phase covers NH steps of 64 k
+// (each stage holds NH halves laid out as gemm_big's 64-k stages, same
+// swizzles), so a phase keeps the matrix cores busy long enough for the
+// other group's reads. Group 0 also loads the A tile of the next phase and
+// group 1 the B tile of the phase after that, so the direct-to-LDS writes
+// are spread over both groups' read phases. Two stages.
 //
 // Phase p (between barriers p and p + 1): group 0 reads step p/2 (p even)
 // or computes step (p-1)/2 (p odd); group 1 is one phase behind. A stage's
@@ -575,15 +577,18 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
 // 0's read of step s and waited for at the end of its compute of step s; B
 // of step s + 2 is issued by group 1 right after its read of step s and
 // waited for at the end of its read of step s + 1.
-template <bool BT, int EPI>
+template <bool BT, int EPI, int BM, int BN, int NH>
 __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, const u16* __restrict__ B,
                                                   void* __restrict__ C, const u16* __restrict__ bias, int M, int N,
                                                   int K, int G) {
-    constexpr int BM = 256, BN = 256, BK = 64, WGN = 4, KC = BK / 8;
-    constexpr int WM = 128, WN = 64, TM = WM / 32, TN = WN / 32;
-    constexpr int LP = BM * BK / 512 / 4;  // 1 KB loads per wavefront per step (of A in group 0, of B in group 1)
+    constexpr int BK = 64, WGN = 4, KC = BK / 8;
+    constexpr int WM = BM / 2, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+    constexpr int LP = BM * BK / 512 / 4;  // 1 KB loads per wavefront per half (of A in group 0, of B in group 1)
+    static_assert(BM == BN && TM >= 1 && TN >= 1 && (BT || BN >= 128), "tile shape");
     constexpr int RPL = 512 / BN, RPA = 512 / BK;
-    constexpr int STAGE = (BM + BN) * BK * 2;
+    constexpr int HALF = (BM + BN) * BK * 2;  // bytes of one 64-k half: A [BM][64], then B
+    constexpr int STAGE = NH * HALF;
+    constexpr int SUB = 4 * NH;  // 16-k substeps per phase
     __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE / 2];
     auto sw = [](int r) { return (r >> 1) & 7; };
 
@@ -598,7 +603,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, con
     const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
 
     // This wavefront's loads: 1 KB each of the A tile (group 0) or the B
-    // tile (group 1), lane offsets relative to the step's first column (A,
+    // tile (group 1), lane offsets relative to the half's first column (A,
     // W) or row (B [K, N]); the buffer base advances with k in scalars.
     uint32_t off[LP];
 #pragma unroll
@@ -615,20 +620,24 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, con
     }
     auto issue = [&](int k0, int stage) {
         const bool a = grp == 0;
-        const long shift = a || BT ? (long)k0 * 2 : (long)k0 * N * 2;
-        const char* base = reinterpret_cast<const char*>(a ? A : B) + shift;
-        i32x4 rs = make_rsrc(base, (uint32_t)((a ? (long)M * K : (long)N * K) * 2 - shift));
 #pragma unroll
-        for (int c = 0; c < 4; c++) rs[c] = __builtin_amdgcn_readfirstlane(rs[c]);  // uniform: keep it in SGPRs
-        const uint32_t dst =
-            __builtin_amdgcn_readfirstlane(lds_base + stage * STAGE + (a ? 0 : BM * BK * 2) + w4 * LP * 1024);
+        for (int h = 0; h < NH; h++) {
+            const int k = k0 + BK * h;
+            const long shift = a || BT ? (long)k * 2 : (long)k * N * 2;
+            const char* base = reinterpret_cast<const char*>(a ? A : B) + shift;
+            i32x4 rs = make_rsrc(base, (uint32_t)((a ? (long)M * K : (long)N * K) * 2 - shift));
 #pragma unroll
-        for (int i = 0; i < LP; i++)
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(dst + i * 1024),
-                         "v"(off[i]), "s"(rs));
+            for (int c = 0; c < 4; c++) rs[c] = __builtin_amdgcn_readfirstlane(rs[c]);  // uniform: keep it in SGPRs
+            const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_base + stage * STAGE + h * HALF +
+                                                                (a ? 0 : BM * BK * 2) + w4 * LP * 1024);
+#pragma unroll
+            for (int i = 0; i < LP; i++)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(dst + i * 1024),
+                             "v"(off[i]), "s"(rs));
+        }
     };
 
-    // LDS byte addresses of this lane's operands in stage 0 (gemm_big's).
+    // LDS byte addresses of this lane's operands in half 0 of stage 0 (gemm_big's).
     uint32_t a_addr[BK / 16], b_addr[TN];
 #pragma unroll
     for (int st = 0; st < BK / 16; st++) {
@@ -646,22 +655,26 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, con
         }
     }
     const char* ldsc = reinterpret_cast<const char*>(lds);
-    half8 av[BK / 16][TM], bv[BK / 16][TN];
+    half8 av[SUB][TM], bv[SUB][TN];
     auto read_step = [&](int stage) {
-        const int so = stage * STAGE;
 #pragma unroll
-        for (int st = 0; st < BK / 16; st++) {
+        for (int h = 0; h < NH; h++) {
+            const int so = stage * STAGE + h * HALF;
 #pragma unroll
-            for (int i = 0; i < TM; i++)
-                av[st][i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 32 * BK * 2);
+            for (int st = 0; st < BK / 16; st++) {
+                const int u = 4 * h + st;
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                if constexpr (BT) {
-                    const int r = wn0 + j * 32 + (lane & 31);
-                    bv[st][j] = *reinterpret_cast<const half8*>(ldsc + so + b_addr[j] + (((2 * st + g) ^ sw(r)) * 16));
-                } else {
-                    const u16* p = reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + 16 * st * BN * 2);
-                    bv[st][j] = __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * BN), 0, 1, 2, 3, 4, 5, 6, 7);
+                for (int i = 0; i < TM; i++)
+                    av[u][i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 32 * BK * 2);
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    if constexpr (BT) {
+                        const int r = wn0 + j * 32 + (lane & 31);
+                        bv[u][j] = *reinterpret_cast<const half8*>(ldsc + so + b_addr[j] + (((2 * st + g) ^ sw(r)) * 16));
+                    } else {
+                        const u16* p = reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + 16 * st * BN * 2);
+                        bv[u][j] = __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * BN), 0, 1, 2, 3, 4, 5, 6, 7);
+                    }
                 }
             }
         }
@@ -675,12 +688,12 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, con
         for (int j = 0; j < TN; j++) acc[i][j] = float16v{};
     auto compute = [&]() {
 #pragma unroll
-        for (int st = 0; st < BK / 16; st++)
+        for (int u = 0; u < SUB; u++)
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[st][i], bv[st][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[u][i], bv[u][j], acc[i][j], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
     };
     // A workgroup barrier that nothing is scheduled across (LDS reads and
@@ -692,13 +705,14 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, con
     };
 
     // Both groups execute 2 nk + 1 barriers.
-    const int nk = K / BK;
+    constexpr int PK = BK * NH;  // k per phase
+    const int nk = K / PK;
     issue(0, 0);
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     bar();
     if (grp == 0) {
         for (int s = 0; s < nk; s++) {
-            if (s + 1 < nk) issue((s + 1) * BK, (s + 1) & 1);
+            if (s + 1 < nk) issue((s + 1) * PK, (s + 1) & 1);
             read_step(s & 1);
             bar();
             compute();
@@ -706,13 +720,13 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, con
             bar();
         }
     } else {
-        if (nk > 1) issue(BK, 1);
+        if (nk > 1) issue(PK, 1);
         bar();
         for (int s = 0; s < nk; s++) {
             read_step(s & 1);
             if (s + 2 < nk) {
-                issue((s + 2) * BK, s & 1);
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(LP));  // B of step s + 1 has landed
+                issue((s + 2) * PK, s & 1);
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(LP * NH));  // B of step s + 1 has landed
             } else {
                 __builtin_amdgcn_s_waitcnt(0x0f70);
             }
@@ -1576,7 +1590,8 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             // each): the ping-pong form when K is whole steps, else one
             // wave's MFMAs cover the other's loads and barrier.
             if (K % 64 == 0)
-                hipLaunchKernelGGL((gemm_pp<BT, EPI>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, C, bias, M, N, K, 4);
+                hipLaunchKernelGGL((gemm_pp<BT, EPI, 256, 256, 1>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, C, bias, M, N, K,
+                                   4);
             else
                 hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4, 64, 2>), dim3(tiles(256, 256)), dim3(512), 0, s, A,
                                    B, B2, C, bias, M, N, K, 4);
@@ -1613,10 +1628,16 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             hipLaunchKernelGGL(skinny_reduce<EPI>, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, split, M,
                                N, C, bias);
         } else if (tiles(128, 128) >= 256 && !BT) {
-            // matmul (B [K, N]) at 128 x 128: 8 wavefronts of 64 x 32 and 3
-            // stages (2048^3: 30.0 -> 26.5 us against 4 wavefronts, 2 stages).
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 4, 64, 3>), dim3(tiles(128, 128)), dim3(512), 0, s, A, B, B2,
-                               C, bias, M, N, K, 4);
+            // matmul (B [K, N]) at 128 x 128: 8 wavefronts of 64 x 32, the
+            // ping-pong form with phases of 128 k when K allows (2048^3:
+            // 25.7 -> 24.8 us), else 3 stages (30.0 -> 26.5 us against 4
+            // wavefronts, 2 stages).
+            if (K % 128 == 0)
+                hipLaunchKernelGGL((gemm_pp<BT, EPI, 128, 128, 2>), dim3(tiles(128, 128)), dim3(512), 0, s, A, B, C, bias,
+                                   M, N, K, 4);
+            else
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 4, 64, 3>), dim3(tiles(128, 128)), dim3(512), 0, s, A,
+                                   B, B2, C, bias, M, N, K, 4);
         } else if (tiles(128, 128) >= 256) {
             hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);

@@ -65,11 +65,13 @@ def test_matmul_large_sampled(n):
     parity("matmul rows", got[rows], want_rows)
 
 
-@pytest.mark.parametrize("m,k,n", [(3900, 1024, 4000), (4000, 1000, 3900), (1000, 1000, 1000)])
+@pytest.mark.parametrize("m,k,n", [(3900, 1024, 4000), (4000, 1000, 3900), (1000, 1000, 1000), (2000, 1024, 2040),
+                                   (2040, 1000, 2000)])
 def test_matmul_tiles_ragged_exact(m, k, n):
     # The 256 x 256 tiles with ragged M and N: the ping-pong form (K % 64 == 0)
     # and the two-stage form (a partial last K step); 32 x 128 tiles (about
-    # 1024^3) with ragged M, N and K. Integer operands make
+    # 1024^3) with ragged M, N and K; 128 x 128 tiles (about 2048^3) in the
+    # ping-pong form (K % 128 == 0) and the three-stage form. Integer operands make
     # every f32 sum exact, so the f16 outputs must equal the rounded integers.
     _say("matmul large tiles", m, k, n)
     rng = np.random.default_rng(m + k)
