@@ -294,7 +294,19 @@ __global__ __launch_bounds__(64 * NWV) void decode_tiles(DecArgs a) {
     // The kv heads of one (b, chunk) are adjacent in launch order, so the
     // pages' token rows (all G heads' 2D-byte slices) are read at one time.
     const int g = blockIdx.x % a.G, c = (blockIdx.x / a.G) % a.NCH, b = blockIdx.x / (a.G * a.NCH);
+    // The length, the query rows and the chunk's table entries (one per lane;
+    // tiles past the table read page 0) in one round trip: none of these
+    // loads depends on another.
     const int n = a.lens[b];
+    half8 qop[D / 32];  // Q^T operand: lane l holds head l%16, d = 32 s + 8 (l/16) .. +8.
+#pragma unroll
+    for (int s = 0; s < D / 32; s++) {
+        u32x4 t = {0, 0, 0, 0};
+        if (col < QPG) t = *reinterpret_cast<const u32x4*>(a.Q + ((long)b * a.H + g * QPG + col) * D + 32 * s + 8 * grp);
+        qop[s] = __builtin_bit_cast(half8, t);
+    }
+    const int page_lo = c * a.CH;
+    const int tab = lane < a.CH && page_lo + lane < a.MP ? a.table[(long)b * a.MP + page_lo + lane] : 0;
     const int npages = n > 0 ? (n + a.P - 1) / a.P : 0;
     const int nact = min((npages + a.CH - 1) / a.CH, a.NCH);
     if (c >= nact) {
@@ -308,17 +320,6 @@ __global__ __launch_bounds__(64 * NWV) void decode_tiles(DecArgs a) {
     const int ntile = (t_end - t_lo) / TT;
     const int nt = wave < ntile ? (ntile - wave + NWV - 1) / NWV : 0;  // tiles wave, wave + NWV, ...
 
-    // Q^T operand: lane l holds head l%16, d = 32 s + 8 (l/16) .. +8.
-    half8 qop[D / 32];
-#pragma unroll
-    for (int s = 0; s < D / 32; s++) {
-        u32x4 t = {0, 0, 0, 0};
-        if (col < QPG) t = *reinterpret_cast<const u32x4*>(a.Q + ((long)b * a.H + g * QPG + col) * D + 32 * s + 8 * grp);
-        qop[s] = __builtin_bit_cast(half8, t);
-    }
-    // The chunk's table entries, one per lane (tiles past the table read page 0).
-    const int page_lo = c * a.CH;
-    const int tab = lane < a.CH && page_lo + lane < a.MP ? a.table[(long)b * a.MP + page_lo + lane] : 0;
 
     // Load offsets (bytes from the tile's first row): load q, lane i fills
     // LDS chunk i % KCH of row q RPL + i / KCH with the logical chunk that
