@@ -1370,15 +1370,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
                     if (j >= nsw || 16 * t + row >= M) xv[j][t][i] = z;
                 }
     }
-    float rsv[MT];  // rs of rows 16 t + row (RS)
-    if constexpr (RS) {
-        ssv_fence(ssv);
-        float* rsb = &red[0][0][0];
-        rs_from_partials(ssv, np.nr, M, K, np.eps, rsb, rsb + 512);
-#pragma unroll
-        for (int t = 0; t < MT; t++) rsv[t] = 16 * t + row < M ? rsb[512 + 16 * t + row] : 0.0f;
-        __syncthreads();  // red is the reduction's again
-    }
+    float rsv[MT];  // rs of rows 16 t + row (RS; formed after the first block's MFMAs)
+    if constexpr (RS) ssv_fence(ssv);
     const char* ldsc = reinterpret_cast<const char*>(lds) + wave * 2 * SLOT;
     int slot = 0;
     for (int b = b0; b < nblk; b += bs, slot ^= 1) {
@@ -1405,6 +1398,14 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
                 for (int t = 0; t < MT; t++)
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, __builtin_bit_cast(half8, xv[j][t][i]), acc[t], 0,
                                                                   0, 0);
+            }
+        }
+        if constexpr (RS) {
+            if (b == b0) {  // (uniform) behind the first block's MFMAs, before red is needed
+                float* rsb = &red[0][0][0];
+                rs_from_partials(ssv, np.nr, M, K, np.eps, rsb, rsb + 512);
+#pragma unroll
+                for (int t = 0; t < MT; t++) rsv[t] = 16 * t + row < M ? rsb[512 + 16 * t + row] : 0.0f;
             }
         }
         // Sum the 8 partial tiles in wavefront order (thread tid < 256: element
