@@ -300,6 +300,34 @@ def test_weights_random_shape_and_scale():
     assert wqkv[0] == np.float16(np.float32(r.uniform()) * s).astype(np.float32)
 
 
+def test_weights_random_draw_order():
+    """Every tensor of Weights::random in the draw order of src/llm/mod.rs:80-108: per layer
+    wqkv, wo, wg, wu, wd (norms are ones, no draws), then embed (f16 of the draw, times 8,
+    rounded again), then lm_head; each matrix draws rows x cols uniforms scaled by
+    1/sqrt(cols) in f32. A swapped pair of draws (wg/wu, embed/lm_head) fails here."""
+    for cfg, seed in ((oracle.Config.tiny(), 7), (oracle.Config.tiny(), 123)):
+        embed, layers, norm, head = oracle.weights_random(cfg, seed)
+        r = oracle.Rng(seed)
+
+        def m(rows, cols):
+            sc = np.float32(1) / np.sqrt(np.float32(cols))
+            return r.tensor("f16", [rows * cols], float(sc))
+
+        d, ff, hd, nh = cfg.dim, cfg.ffn, cfg.head_dim, cfg.heads
+        want_layers = []
+        for _ in range(cfg.layers):
+            ones = np.ones(d, np.float16)
+            wqkv, wo = m(cfg.qkv(), d), m(d, nh * hd)
+            wg, wu, wd = m(ff, d), m(ff, d), m(d, ff)
+            want_layers += [ones, wqkv, wo, ones, wg, wu, wd]
+        want_embed = (m(cfg.vocab, d).astype(np.float32) * np.float32(8)).astype(np.float16)
+        want_head = m(cfg.vocab, d)
+        assert np.array_equal(layers.view(np.uint16), np.concatenate(want_layers).view(np.uint16))
+        assert np.array_equal(embed.view(np.uint16), want_embed.view(np.uint16))
+        assert np.array_equal(head.view(np.uint16), want_head.view(np.uint16))
+        assert (norm == 1).all()
+
+
 def _np_forward(cfg, w, tokens):
     """An independent f64 numpy model of src/llm/reference.rs."""
     embed, layers, norm, head = (a.astype(np.float64) for a in w)
