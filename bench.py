@@ -1,7 +1,7 @@
 """Benchmark of tessel's kernel hot path on one MI355X.
 
-A step is one launch of the fp16 GEMM 4096x4096x4096 (BASELINE.json
-configs[1]; A, B ~ N(0,1)/sqrt(K) f16, f32 accumulation, f16 out), inputs
+A step is one launch of the fp16 GEMM 4096x4096x4096 (the headline
+workload; A, B ~ N(0,1)/sqrt(K) f16, f32 accumulation, f16 out), inputs
 resident in HBM. W untimed warm-up steps, then K steps timed with HIP
 events on the library's stream, bracketed by stream synchronisation.
 `value` is TFLOP/s (2MNK per step). The same JSON line carries:
@@ -10,7 +10,7 @@ events on the library's stream, bracketed by stream synchronisation.
                 the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summaries;
   cpu_baseline  tessel's interpreter semantics (the oracle's C++
                 restatement) on a bounded sample of the same GEMM's programs;
-  cases         the other BASELINE configs measured the same way: GEMM
+  cases         the other benchmark workloads measured the same way: GEMM
                 1024^3/2048^3, causal FlashAttention H32 D64 S 512..4096,
                 paged GQA decode (GB/s against 8 TB/s), paged_attention (G = H),
                 the engine's prefill_attention and its five projections at
@@ -186,7 +186,7 @@ def attention_case(T, s, seed=1):
 
 
 def decode_inputs(seed=2, b=64, h=32, g=8, d=128, p=16):
-    """BASELINE config 4's inputs: lens ~ U[128, 4096], pages by seeded
+    """The paged GQA decode inputs: lens ~ U[128, 4096], pages by seeded
     permutation into int32 tables, KV pool N(0,1) f16. Returns q, kc, vc,
     table, lens, the bytes a call must move, and the context tokens."""
     rng = np.random.default_rng(seed)
@@ -208,7 +208,7 @@ def decode_inputs(seed=2, b=64, h=32, g=8, d=128, p=16):
 
 
 def decode_case(T, seed=2):
-    """BASELINE config 4 on the GPU: one decode_attention launch per step."""
+    """Paged GQA decode on the GPU: one decode_attention launch per step."""
     q, kc, vc, table, lens, nbytes, toks = decode_inputs(seed)
     b, h, d = q.shape
     bufs = [T.tensor(q), T.tensor(kc), T.tensor(vc), T.tensor(table), T.tensor(lens), T.alloc(q.nbytes),
@@ -272,7 +272,7 @@ def rows_case(T, kind):
 
 def prefill_case(T, seed=4, lens=(512, 512), h=32, g=4, d=64):
     """kernels/llm.tl prefill_attention at the engine's prefill step
-    (two 512-token prompts packed into 1024 rows)."""
+    (the engine workload: two 512-token prompts packed into 1024 rows)."""
     rng = np.random.default_rng(seed)
     t = sum(lens)
     q = f16(rng.standard_normal((t, h, d), np.float32))
@@ -284,7 +284,7 @@ def prefill_case(T, seed=4, lens=(512, 512), h=32, g=4, d=64):
     return Timed(T, kern, bufs), flops
 
 
-# The TinyLlama projections (dim 2048, QKV 2560, FFN 5632,
+# The TinyLlama projections (the engine workload: dim 2048, QKV 2560, FFN 5632,
 # vocab 32000) as the engine runs them: name, K, N.
 PROJ = (("linear", 2048, 2560, "qkv"), ("linear_residual", 2048, 2048, "o"), ("gate_up", 2048, 5632, "gate_up"),
         ("linear_residual", 5632, 2048, "down"), ("logits", 2048, 32000, "logits"))
@@ -346,7 +346,7 @@ def paged_case(T, seed=3, b=16, h=32, d=128, p=16):
 
 
 def llm_case(T, seqs=32, prompt=512, new=128, graphs=True):
-    """TinyLlama-1.1B shape, random fp16 weights, 32
+    """The engine workload: TinyLlama-1.1B shape, random fp16 weights, 32
     prompts of 512 random ids, 128 greedy steps under continuous batching."""
     cfg = T.Config.tinyllama()
     t0 = time.perf_counter()

@@ -166,7 +166,7 @@ def test_close_then_launch():
 
 
 def _tinyllama_engine(seqs=32, prompt=512, new=128, graphs=True):
-    # BASELINE config 5's engine: TinyLlama-1.1B shape, Weights::random(7)
+    # The headline engine workload: TinyLlama-1.1B shape, Weights::random(7)
     # (the library's generator, equal to the oracle's bit for bit:
     # tests/test_abi.py), page 16, 1024-token steps.
     cfg = T.Config.tinyllama()

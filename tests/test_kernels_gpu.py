@@ -1,6 +1,6 @@
 """The HIP kernels, launched through the C ABI, against the CPU oracle on
 identical seeded inputs: the reference's own test shapes (tests/interp.rs,
-tests/emu.rs, tests/llm.rs:108-187) and the BASELINE configs. Tolerance for
+tests/emu.rs, tests/llm.rs:108-187) and the benchmark workloads. Tolerance for
 float outputs (written in refs.parity): relative Frobenius error <= 1e-3
 and max |diff| <= 2e-2; integer, index and copy results bit-exact."""
 
@@ -49,7 +49,7 @@ def test_matmul_exact_integers():
 
 @pytest.mark.parametrize("n", [1024, 2048, 4096])
 def test_matmul_large_sampled(n):
-    # A, B ~ N(0,1)/sqrt(K); checked at 512 sampled entries
+    # The benchmark GEMM inputs: A, B ~ N(0,1)/sqrt(K); checked at 512 sampled entries
     # against f64 (as src/bench.rs:86-98 does) and, on a block of rows, against the oracle.
     _say("matmul large", n)
     rng = np.random.default_rng(n)
@@ -234,7 +234,7 @@ def test_flash_attention_vs_oracle(h, s, d):
 
 @pytest.mark.parametrize("s", [512, 1024])
 def test_flash_attention_baseline_shapes(s):
-    # BASELINE config 3 (H 32, D 64) against the oracle.
+    # The benchmark attention shape (H 32, D 64) against the oracle.
     _say("flash baseline", s)
     rng = np.random.default_rng(s)
     q, k, v = (rng.standard_normal((32, s, 64)).astype(np.float16) for _ in range(3))
@@ -286,7 +286,7 @@ def test_flash_attention_long_sampled(s):
 
 @pytest.mark.parametrize("s", [2048, 4096])
 def test_flash_attention_long_whole_heads_vs_oracle(s):
-    # BASELINE config 3 at its long sizes: the 32-head launch, with four
+    # The benchmark attention shape at its long sizes: the 32-head launch, with four
     # whole heads (every row) against the interpreter restatement of
     # kernels/attention.tl:4-24 (heads are independent programs, so the
     # oracle runs on just those heads' slices).
@@ -347,7 +347,7 @@ def test_paged_attention_long_tables(b, h, d, p, lo, hi):
 
 
 def decode_case(seed, b=64, h=32, g=8, d=128, p=16, lo=128, hi=4096, mp=None):
-    """lens ~ U[lo, hi], pages assigned by a seeded
+    """The benchmark decode workload: lens ~ U[lo, hi], pages assigned by a seeded
     permutation into int32 block tables, KV pool N(0,1) f16."""
     rng = np.random.default_rng(seed)
     lens = rng.integers(lo, hi + 1, b).astype(np.int32)

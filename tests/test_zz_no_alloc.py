@@ -55,7 +55,7 @@ def _both(q, kc, vc, table, lens, scale):
 
 
 @pytest.mark.parametrize("cases", [
-    # BASELINE config 4 (balanced stream path), then a smaller call (fewer
+    # The benchmark decode shape (balanced stream path), then a smaller call (fewer
     # sequences, shorter tables: the chunked path) on the same scratch.
     [(1, 64, 32, 8, 128, 16, 128, 4096), (2, 12, 32, 8, 128, 16, 100, 1500)],
     # The TinyLlama engine's decode shape (D 64, G 4), then a smaller one.
