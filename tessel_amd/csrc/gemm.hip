@@ -1158,33 +1158,40 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         for (int t = 0; t < MT; t++) rope_cs(ep, rpos[t], n, rc[t], rsn[t]);
     }
     // Sum the 8 partial tiles through LDS in wavefront order; thread tid < 256
-    // keeps element tid (register tid/64 of lane tid%64) of each.
+    // keeps element tid (register tid/64 of lane tid%64) of each. All MT
+    // tiles go at once into the W block's LDS, free once every wavefront's
+    // MFMAs are done: [MT][wave][4][64] partials, then [MT][4][64] for the
+    // partner exchange.
+    static_assert(MT * (SK_WAVES + 1) * 256 * 4 <= WB, "the reduction fits the W block");
+    float* rd = reinterpret_cast<float*>(lds);
+    float* xc = rd + MT * SK_WAVES * 256;
+    __syncthreads();  // every wavefront's W and X reads are done
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) rd[((t * SK_WAVES + wave) * 4 + r) * 64 + lane] = acc[t][r];
+    __syncthreads();
     float sum[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) {
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < 4; r++) red[wave][r][lane] = acc[t][r];
-        __syncthreads();
         float v = 0.0f;
         if (tid < 256)
 #pragma unroll
-            for (int w = 0; w < SK_WAVES; w++) v += red[w][tid >> 6][tid & 63];
+            for (int w = 0; w < SK_WAVES; w++) v += rd[(t * SK_WAVES + w) * 256 + tid];
         sum[t] = v;
     }
     // Element (r, l): block row 4 (l / 16) + r, m = 16 t + l % 16. For
     // gate_up, rows 0..7 are gate rows and 8..15 their up partners, which
-    // sit 32 lanes on: exchanged through red.
+    // sit 32 lanes on: exchanged through LDS.
     const int r = tid >> 6, l = tid & 63;
     float up[MT];
     if constexpr (DUAL) {
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
-            __syncthreads();
-            if (tid < 256) red[0][r][l] = sum[t];
-            __syncthreads();
-            up[t] = tid < 256 && l < 32 ? red[0][r][l + 32] : 0.0f;
-        }
+        for (int t = 0; t < MT; t++)
+            if (tid < 256) xc[t * 256 + tid] = sum[t];
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < MT; t++) up[t] = tid < 256 && l < 32 ? xc[t * 256 + r * 64 + l + 32] : 0.0f;
     }
     if constexpr (RS) {
         // rs[m] (the ring is free: every wavefront is past the reduction's
@@ -1205,8 +1212,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         // halves go through LDS, then each token row leaves as two 16-byte
         // stores (per element 2-byte stores would scatter over 16 rows).
         static_assert(16 * MT * 16 * 2 <= (int)sizeof(red), "staging fits the reduction buffer");
-        u16 (*yb)[16] = reinterpret_cast<u16 (*)[16]>(&red[0][0][0]);  // [16 MT][16]
-        __syncthreads();  // the exchange above has read red
+        u16 (*yb)[16] = reinterpret_cast<u16 (*)[16]>(&red[0][0][0]);  // [16 MT][16] (red is not the reduction's)
         if (tid < 256 && l < 32) {
 #pragma unroll
             for (int t = 0; t < MT; t++) {
@@ -1227,10 +1233,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     if constexpr (R8) {
         // R += Y for the block's 8 columns; np.y = f16(R np.w); then the
         // squares of the new values summed per row in column order (through
-        // red, now free).
-        float* sq = &red[0][0][0];  // [MT][8 columns][16 rows]
-        static_assert(MT * 8 * 16 <= SK_WAVES * 4 * 64, "squares fit the reduction buffer");
-        __syncthreads();  // every wavefront has read red
+        // red).
+        float* sq = &red[0][0][0];  // [MT][8 columns][16 rows] (red is not the reduction's)
+        static_assert(MT * 8 * 16 <= SK_WAVES * 4 * 64, "squares fit the staging buffer");
         if (tid < 256 && l < 32) {
 #pragma unroll
             for (int t = 0; t < MT; t++) {
@@ -1299,7 +1304,12 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
     constexpr int SLOT = 16 * SPW * 128;     // LDS bytes of one block's segments
     static_assert(MT <= 2, "X stays in registers");
     __shared__ __attribute__((aligned(16))) u16 lds[SK_WAVES * 2 * SLOT / 2];
-    __shared__ float red[SK_WAVES][4][64];
+    // Every wavefront's partial tiles of both row tiles at once, gate_up's
+    // partner exchange beside them, and the row scales' scratch: two
+    // barriers per block.
+    __shared__ float red[MT][SK_WAVES][4][64];
+    __shared__ float xch[DUAL ? MT : 1][4][64];
+    __shared__ float rsl[RS ? 512 + 32 : 1];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row = lane & 15, g = lane >> 4;
@@ -1401,38 +1411,42 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
             }
         }
         if constexpr (RS) {
-            if (b == b0) {  // (uniform) behind the first block's MFMAs, before red is needed
-                float* rsb = &red[0][0][0];
-                rs_from_partials(ssv, np.nr, M, K, np.eps, rsb, rsb + 512);
+            if (b == b0) {  // (uniform) behind the first block's MFMAs
+                rs_from_partials(ssv, np.nr, M, K, np.eps, rsl, rsl + 512);
 #pragma unroll
-                for (int t = 0; t < MT; t++) rsv[t] = 16 * t + row < M ? rsb[512 + 16 * t + row] : 0.0f;
+                for (int t = 0; t < MT; t++) rsv[t] = 16 * t + row < M ? rsl[512 + 16 * t + row] : 0.0f;
             }
         }
         // Sum the 8 partial tiles in wavefront order (thread tid < 256: element
-        // tid), then gate_up's partner exchange and the epilogue.
+        // tid), then gate_up's partner exchange and the epilogue. The previous
+        // block's reads of red and xch are behind barriers every wavefront
+        // has passed: red's behind this block's exchange barrier (gate_up)
+        // or the barrier after the sums; xch's behind this block's first.
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[t][wave][r][lane] = acc[t][r];
+        __syncthreads();
         float sum[MT];
 #pragma unroll
         for (int t = 0; t < MT; t++) {
-            __syncthreads();
-#pragma unroll
-            for (int r = 0; r < 4; r++) red[wave][r][lane] = acc[t][r];
-            __syncthreads();
             float v = 0.0f;
             if (tid < 256)
 #pragma unroll
-                for (int w = 0; w < SK_WAVES; w++) v += red[w][tid >> 6][tid & 63];
+                for (int w = 0; w < SK_WAVES; w++) v += red[t][w][tid >> 6][tid & 63];
             sum[t] = v;
         }
         const int r = tid >> 6, l = tid & 63;
         float up[MT];
         if constexpr (DUAL) {
 #pragma unroll
-            for (int t = 0; t < MT; t++) {
-                __syncthreads();
-                if (tid < 256) red[0][r][l] = sum[t];
-                __syncthreads();
-                up[t] = tid < 256 && l < 32 ? red[0][r][l + 32] : 0.0f;
-            }
+            for (int t = 0; t < MT; t++)
+                if (tid < 256) xch[t][r][l] = sum[t];
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < MT; t++) up[t] = tid < 256 && l < 32 ? xch[t][r][l + 32] : 0.0f;
+        } else {
+            __syncthreads();
         }
         if (tid < 256 && (!DUAL || l < 32)) {
             const int n0 = b * rpb;
