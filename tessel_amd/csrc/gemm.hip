@@ -1417,45 +1417,43 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
                 for (int t = 0; t < MT; t++) rsv[t] = 16 * t + row < M ? rsl[512 + 16 * t + row] : 0.0f;
             }
         }
-        // Sum the 8 partial tiles in wavefront order (thread tid < 256: element
-        // tid), then gate_up's partner exchange and the epilogue. The previous
-        // block's reads of red and xch are behind barriers every wavefront
-        // has passed: red's behind this block's exchange barrier (gate_up)
-        // or the barrier after the sums; xch's behind this block's first.
+        // Sum the 8 partial tiles in wavefront order, thread tid element
+        // tid % 256 of row tile tid / 256 (MT = 2: every thread one), then
+        // gate_up's partner exchange and the epilogue, one output per thread.
+        // The previous block's reads of red and xch are behind barriers every
+        // wavefront has passed: red's behind this block's exchange barrier
+        // (gate_up) or the barrier after the sums; xch's behind this block's
+        // first.
 #pragma unroll
         for (int t = 0; t < MT; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) red[t][wave][r][lane] = acc[t][r];
         __syncthreads();
-        float sum[MT];
+        const int te = tid >> 8, ie = tid & 255;  // element (r, l) = (ie / 64, ie % 64) of row tile te
+        const bool has = te < MT;
+        float se = 0.0f;
+        if (has)
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
-            float v = 0.0f;
-            if (tid < 256)
-#pragma unroll
-                for (int w = 0; w < SK_WAVES; w++) v += red[t][w][tid >> 6][tid & 63];
-            sum[t] = v;
-        }
-        const int r = tid >> 6, l = tid & 63;
-        float up[MT];
+            for (int w = 0; w < SK_WAVES; w++) se += red[te < MT ? te : 0][w][ie >> 6][ie & 63];
+        // Element (r, l): block row 4 (l / 16) + r, m = 16 te + l % 16 (so l % 16
+        // is this thread's row: rsv applies). gate_up: rows 0..7 are gate rows
+        // and 8..15 their up partners, 32 lanes on.
+        const int n0 = b * rpb;
+        const float rs_t = [&](int t) { return RS ? (MT == 2 && t ? rsv[MT - 1] : rsv[0]) : 1.0f; }(DUAL ? tid >> 7 : te);
         if constexpr (DUAL) {
-#pragma unroll
-            for (int t = 0; t < MT; t++)
-                if (tid < 256) xch[t][r][l] = sum[t];
+            if (has) xch[te < MT ? te : 0][ie >> 6][ie & 63] = se;
             __syncthreads();
-#pragma unroll
-            for (int t = 0; t < MT; t++) up[t] = tid < 256 && l < 32 ? xch[t][r][l + 32] : 0.0f;
+            if (tid < 128 * MT) {  // output tid: gate element (q / 32, q % 32) of row tile tid / 128, q = tid % 128
+                const int t = tid >> 7, q = tid & 127, r = q >> 5, l = q & 31;
+                const int n = n0 + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
+                if (m < M && n < N) sk_store<EPI>(C, bias, N, m, n, xch[t][r][l] * rs_t, xch[t][r][l + 32] * rs_t);
+            }
         } else {
             __syncthreads();
-        }
-        if (tid < 256 && (!DUAL || l < 32)) {
-            const int n0 = b * rpb;
-#pragma unroll
-            for (int t = 0; t < MT; t++) {
-                const int n = n0 + 4 * (l >> 4) + r, m = 16 * t + (l & 15);
-                if (m >= M || n >= N) continue;
-                if constexpr (RS) sk_store<EPI>(C, bias, N, m, n, sum[t] * rsv[t], DUAL ? up[t] * rsv[t] : 0.0f);
-                else sk_store<EPI>(C, bias, N, m, n, sum[t], DUAL ? up[t] : 0.0f);
+            if (has) {
+                const int r = ie >> 6, l = ie & 63;
+                const int n = n0 + 4 * (l >> 4) + r, m = 16 * te + (l & 15);
+                if (m < M && n < N) sk_store<EPI>(C, bias, N, m, n, se * rs_t, 0.0f);
             }
         }
         // The block after next into the slot just read. Issued after the
