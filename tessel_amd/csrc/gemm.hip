@@ -913,14 +913,14 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const u16* __restri
 // The skinny product with both operands staged in LDS (K % 128 == 0). A
 // workgroup owns a block of 16 rows of W (gate_up: 8 rows of Wg and the same
 // 8 rows of Wu) over a slice of at most SL_KS k values:
-// - W: at the start, every load of the block at once, as direct-to-LDS
-//   loads of 1 KB runs of a row's slice (whole 128-byte lines, in address
-//   order). Chunk c (16 bytes) of row r sits at position c ^ (r & 15) of its
-//   LDS row, so the 16 rows an operand read touches fall in distinct bank
-//   groups.
-// - X: each wavefront takes interleaved 64-wide k steps and loads a step's
-//   X rows (16 MT x 128 bytes, 8 whole lines per load) into its own LDS ring
-//   of XD stages, chunk c of row r at position c ^ ((r >> 1) & 7).
+// - each wavefront takes interleaved 64-wide k steps;
+// - W: at the start, every step of the block at once, each wavefront loading
+//   its own steps' rows (8 rows x 128 bytes, whole lines, per direct-to-LDS
+//   load), so a wavefront starts as soon as its first step has landed;
+// - X: a step's X rows (16 MT x 128 bytes, 8 whole lines per load) into the
+//   wavefront's own LDS ring of XD stages;
+// - in both, chunk c (16 bytes) of row r sits at position c ^ ((r >> 1) & 7),
+//   so the 16 rows an operand read touches fall in distinct bank groups.
 // Y^T (16 n x 16 m) += W (16 n x 32 k) X^T (32 k x 16 m) on
 // v_mfma_f32_16x16x32_f16; the 8 partial tiles are summed in LDS in
 // wavefront order, then the epilogue (or the split layout of gemm_skinny).
@@ -1022,6 +1022,18 @@ TSL_DEV void ssv_fence(float (&ssv)[16]) {
     for (int i = 0; i < 16; i++) asm volatile("" : "+v"(ssv[i]));
 }
 
+// s_waitcnt vmcnt(n) for a run-time n (the instruction takes an immediate).
+TSL_DEV void sk_vm_wait(int n) {
+    switch (n) {
+#define SK_VM_CASE(k) case k: __builtin_amdgcn_s_waitcnt(vmcnt_imm(k)); break;
+        SK_VM_CASE(1) SK_VM_CASE(2) SK_VM_CASE(3) SK_VM_CASE(4) SK_VM_CASE(5) SK_VM_CASE(6) SK_VM_CASE(7)
+        SK_VM_CASE(8) SK_VM_CASE(9) SK_VM_CASE(10) SK_VM_CASE(11) SK_VM_CASE(12) SK_VM_CASE(13) SK_VM_CASE(14)
+        SK_VM_CASE(15) SK_VM_CASE(16) SK_VM_CASE(17) SK_VM_CASE(18) SK_VM_CASE(19) SK_VM_CASE(20)
+#undef SK_VM_CASE
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;  // (0, or more than listed: wait for all)
+    }
+}
+
 // R8 (linear_residual_prenorm, EPI_RESID): blocks of 8 rows of W over the
 // whole K (up to 2 SL_KS, the same LDS); after R += Y the block writes
 // np.y = f16(R np.w) for its 8 columns and the per-row sums of squares of
@@ -1053,7 +1065,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     const int n0 = blockIdx.x * (DUAL || R8 ? 8 : 16);
     const int nb = K / 128, S = SPLIT ? gridDim.y : 1, ks = SPLIT ? blockIdx.y : 0;
     const int b0 = ks * nb / S, b1 = (ks + 1) * nb / S;
-    const int k0 = 128 * b0, KS = 128 * (b1 - b0), cpr = KS / 8, nst = KS / 64;
+    const int k0 = 128 * b0, KS = 128 * (b1 - b0), nst = KS / 64;
     const uint32_t lds_w = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
     const uint32_t lds_x = lds_w + WB + wave * XD * XS;
     // The rotary epilogue's positions and cache slots, loaded before the
@@ -1072,28 +1084,34 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     // The consumer's partial sums of squares, before any W load.
     float ssv[RS ? 16 : 1];
     if constexpr (RS) ssv_load(np.ss, np.nr, M, ssv);
-    // W block: 16 cpr chunks (R8: 8 cpr); load q covers linear chunks 64 q ..
-    // 64 q + 63 (row p / cpr, position p % cpr). Rows past N read as zero.
-    {
-        const int rows = min(DUAL || R8 ? 8 : 16, N - n0);
-        const uint32_t range = (uint32_t)(((long)(rows - 1) * K + KS) * 2);
-        // First rows of the block's two halves (rotary pairs: within one head of W).
-        const long ra = ROPE ? (long)(n0 / ep.D2) * ep.D + n0 % ep.D2 : n0;
-        const i32x4 rw = make_rsrc(W + ra * K + k0, range);
-        const i32x4 rw2 = make_rsrc(ROPE ? W + (ra + ep.D2) * K + k0 : (DUAL ? W2 : W) + (size_t)n0 * K + k0, range);
-        const int nq = (R8 ? 8 : 16) * cpr / 64;
-        for (int q = wave; q < nq; q += SK_WAVES) {
-            const int p = 64 * q + lane, r = p / cpr, pos = p - r * cpr;
+    // W block, by k step: step st (of this slice) holds the block's WR rows x
+    // 64 k at lds_w + st WSB, row r at r 128 with chunk c at c ^ ((r >> 1) & 7)
+    // (the X stages' layout). Each wavefront loads the steps it multiplies
+    // (st = wave + 8 u), 8 rows per 1 KB load, so it waits for nobody else's
+    // loads. Rows past N read as zero.
+    constexpr int WR = R8 ? 8 : 16, WSB = WR * 128, WL = WR / 8;
+    const int rows_n = min(DUAL || R8 ? 8 : 16, N - n0);
+    const uint32_t wrange = (uint32_t)(((long)(rows_n - 1) * K + KS) * 2);
+    // First rows of the block's two halves (rotary pairs: within one head of W).
+    const long ra = ROPE ? (long)(n0 / ep.D2) * ep.D + n0 % ep.D2 : n0;
+    const i32x4 rw = make_rsrc(W + ra * K + k0, wrange);
+    const i32x4 rw2 = make_rsrc(ROPE ? W + (ra + ep.D2) * K + k0 : (DUAL ? W2 : W) + (size_t)n0 * K + k0, wrange);
+    auto load_w = [&](int st) {
+#pragma unroll
+        for (int h = 0; h < WL; h++) {
+            const int r = 8 * h + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
             const int rr = DUAL ? r & 7 : r;  // row within its matrix
-            const uint32_t off = (uint32_t)((rr * K + 8 * (pos ^ (r & 15))) * 2);
-            if (DUAL && q * 64 >= 8 * cpr)  // rows 8..15: Wu (uniform: 8 cpr is a multiple of 64)
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds_w + q * 1024),
-                             "v"(off), "s"(rw2));
+            const uint32_t off = (uint32_t)((rr * K + 64 * st + 8 * c) * 2);
+            if (DUAL && h == 1)  // rows 8..15: Wu (or the rotary partners)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds_w + st * WSB + h * 1024),
+                             "v"(off), "s"(rw2)
+                             : "memory");
             else
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds_w + q * 1024),
-                             "v"(off), "s"(rw));
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(lds_w + st * WSB + h * 1024),
+                             "v"(off), "s"(rw)
+                             : "memory");
         }
-    }
+    };
     // X step st into stage slot: load j covers rows 8 j .. 8 j + 7, lane l
     // row 8 j + l / 8 at position l % 8. Rows past M read as zero.
     const i32x4 rx = make_rsrc(X, (uint32_t)((long)M * K * 2));
@@ -1111,32 +1129,46 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         }
     };
     const int mysteps = nst > wave ? (nst - wave + SK_WAVES - 1) / SK_WAVES : 0;
+    // Issue order: W(0) X(0) .. W(XD-1) X(XD-1), then W(XD) .. W(mysteps-1);
+    // X(u + XD) after step u's MFMAs.
 #pragma unroll
     for (int u = 0; u < XD; u++)
-        if (u < mysteps) load_x(wave + SK_WAVES * u, u);
+        if (u < mysteps) {
+            load_w(wave + SK_WAVES * u);
+            load_x(wave + SK_WAVES * u, u);
+        }
+    for (int u = XD; u < mysteps; u++) load_w(wave + SK_WAVES * u);
+    // Loads issued after X(u) by the time step u waits for it.
+    auto after_x = [&](int u) {
+        int n = 0;
+        if (u < XD) {
+            for (int v = u + 1; v < min(XD, mysteps); v++) n += WL + XL;
+            n += WL * max(0, mysteps - XD);
+        }
+        for (int v = max(0, u - XD + 1); v < u; v++)
+            if (v + XD < mysteps) n += XL;
+        return n;
+    };
 
     float4v acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) acc[t] = float4v{};
     const char* ldsc = reinterpret_cast<const char*>(lds);
-    const char* wrow = ldsc + (R8 ? row & 7 : row) * KS * 2;  // (R8: rows 8..15 repeat 0..7, sums dropped)
+    const int wr = R8 ? row & 7 : row;  // (R8: rows 8..15 repeat 0..7, sums dropped)
+    const char* wrow = ldsc + wr * 128;
     const char* xbase = ldsc + WB + wave * XD * XS;
 #pragma unroll
     for (int u = 0; u < MAXU; u++) {
         if (u >= mysteps) break;
-        // Wait for step u's X (later stages may still fly); the first wait
-        // also covers this wavefront's W loads, and the barrier everyone's.
-        const int ahead = min(XD - 1, mysteps - 1 - u);
-        if (ahead > 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(XL));
-        else __builtin_amdgcn_s_waitcnt(0x0f70);
+        // Wait for step u's W and X (issued before X(u)); later loads may fly.
+        sk_vm_wait(after_x(u));
         asm volatile("" ::: "memory");  // no LDS read moves above the wait
-        if (u == 0) __syncthreads();
         const int st = wave + SK_WAVES * u, slot = u % XD;
         const char* xs = xbase + slot * XS;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int c = 8 * st + 4 * i + g;
-            const half8 w = *reinterpret_cast<const half8*>(wrow + 16 * (c ^ row));
+            const int c = 4 * i + g;
+            const half8 w = *reinterpret_cast<const half8*>(wrow + st * WSB + 16 * (c ^ ((wr >> 1) & 7)));
             const int xc = 4 * i + g;
 #pragma unroll
             for (int t = 0; t < MT; t++) {
@@ -1146,10 +1178,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
             }
         }
         if (u + XD < mysteps) load_x(st + SK_WAVES * XD, slot);
-    }
-    if (mysteps == 0) {  // no k step here, but a share of the W loads: land them, then the barrier
-        __builtin_amdgcn_s_waitcnt(0x0f70);
-        __syncthreads();
     }
     float rc[ROPE ? MT : 1], rsn[ROPE ? MT : 1];
     if constexpr (ROPE) {
