@@ -1084,6 +1084,27 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     // The consumer's partial sums of squares, before any W load.
     float ssv[RS ? 16 : 1];
     if constexpr (RS) ssv_load(np.ss, np.nr, M, ssv);
+    // R8: the epilogue's residual values and norm weights, loaded first (so
+    // every wait of the stream covers them) instead of behind the reduction:
+    // thread (r = wave < 4, l < 32) owns column n0 + 4 (l / 16) + r of rows
+    // 16 t + l % 16. Written out like the stream's loads; lanes without an
+    // element read column n0 of row 0.
+    float rv[R8 ? MT : 1];
+    uint32_t wnv = 0;
+    if constexpr (R8) {
+        if (wave < 4) {
+            const int j = 4 * ((lane & 31) >> 4) + wave, n = n0 + j;
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int m = 16 * t + (lane & 15);
+                const bool ok = lane < 32 && m < M && n < N;
+                const float* o = reinterpret_cast<const float*>(C) + (ok ? (size_t)m * N + n : (size_t)n0);
+                asm volatile("global_load_dword %0, %1, off" : "=v"(rv[t]) : "v"(o));
+            }
+            const u16* wp = np.w + (lane < 32 && n < N ? n : n0);
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(wnv) : "v"(wp));
+        }
+    }
     // W block, by k step: step st (of this slice) holds the block's WR rows x
     // 64 k at lds_w + st WSB, row r at r 128 with chunk c at c ^ ((r >> 1) & 7)
     // (the X stages' layout). Each wavefront loads the steps it multiplies
@@ -1264,6 +1285,10 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         // red).
         float* sq = &red[0][0][0];  // [MT][8 columns][16 rows] (red is not the reduction's)
         static_assert(MT * 8 * 16 <= SK_WAVES * 4 * 64, "squares fit the staging buffer");
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // (the prefetched values: landed long ago)
+#pragma unroll
+        for (int t = 0; t < MT; t++) asm volatile("" : "+v"(rv[t]));
+        asm volatile("" : "+v"(wnv));
         if (tid < 256 && l < 32) {
 #pragma unroll
             for (int t = 0; t < MT; t++) {
@@ -1271,9 +1296,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
                 float nv = 0.0f;
                 if (m < M && n < N) {
                     float* o = reinterpret_cast<float*>(C) + (size_t)m * N + n;
-                    nv = *o + sum[t];
+                    nv = rv[t] + sum[t];
                     *o = nv;
-                    float yv = nv * h2f(np.w[n]);
+                    float yv = nv * h2f((u16)wnv);
                     asm volatile("" : "+v"(yv));  // rounded to f32, then to f16 (no fused multiply-convert)
                     np.y[(size_t)m * N + n] = f2h(yv);
                 }
