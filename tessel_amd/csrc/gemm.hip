@@ -1178,8 +1178,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     const int wr = R8 ? row & 7 : row;  // (R8: rows 8..15 repeat 0..7, sums dropped)
     const char* wrow = ldsc + wr * 128;
     const char* xbase = ldsc + WB + wave * XD * XS;
-#pragma unroll
-    for (int u = 0; u < MAXU; u++) {
+    for (int u = 0; u < MAXU; u++) {  // (a run-time trip count: not unrolled)
         if (u >= mysteps) break;
         // Wait for step u's W and X (issued before X(u)); later loads may fly.
         sk_vm_wait(after_x(u));
