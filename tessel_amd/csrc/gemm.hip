@@ -1086,22 +1086,20 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     if constexpr (RS) ssv_load(np.ss, np.nr, M, ssv);
     // R8: the epilogue's residual values and norm weights, loaded first (so
     // every wait of the stream covers them) instead of behind the reduction:
-    // thread (r = wave < 4, l < 32) owns column n0 + 4 (l / 16) + r of rows
-    // 16 t + l % 16. Written out like the stream's loads; lanes without an
-    // element read column n0 of row 0.
-    float rv[R8 ? MT : 1];
+    // thread tid < 128 MT owns one output, (r, l) = ((tid % 128) / 32, tid % 32)
+    // of row tile t = tid / 128: column n0 + 4 (l / 16) + r, row 16 t + l % 16.
+    // Written out like the stream's loads; threads without an element read
+    // column n0 of row 0.
+    const int et = tid >> 7, er = (tid & 127) >> 5, el = tid & 31;  // (R8)
+    const int ej = 4 * (el >> 4) + er, em = 16 * et + (el & 15);
+    float rv = 0.0f;
     uint32_t wnv = 0;
     if constexpr (R8) {
-        if (wave < 4) {
-            const int j = 4 * ((lane & 31) >> 4) + wave, n = n0 + j;
-#pragma unroll
-            for (int t = 0; t < MT; t++) {
-                const int m = 16 * t + (lane & 15);
-                const bool ok = lane < 32 && m < M && n < N;
-                const float* o = reinterpret_cast<const float*>(C) + (ok ? (size_t)m * N + n : (size_t)n0);
-                asm volatile("global_load_dword %0, %1, off" : "=v"(rv[t]) : "v"(o));
-            }
-            const u16* wp = np.w + (lane < 32 && n < N ? n : n0);
+        if (wave < 2 * MT) {  // (uniform)
+            const bool ok = em < M && n0 + ej < N;
+            const float* o = reinterpret_cast<const float*>(C) + (ok ? (size_t)em * N + n0 + ej : (size_t)n0);
+            asm volatile("global_load_dword %0, %1, off" : "=v"(rv) : "v"(o));
+            const u16* wp = np.w + (n0 + ej < N ? n0 + ej : n0);
             asm volatile("global_load_ushort %0, %1, off" : "=v"(wnv) : "v"(wp));
         }
     }
@@ -1223,7 +1221,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
 #pragma unroll
     for (int t = 0; t < MT; t++) {
         float v = 0.0f;
-        if (tid < 256)
+        if (!R8 && tid < 256)  // (R8 sums its own element below)
 #pragma unroll
             for (int w = 0; w < SK_WAVES; w++) v += rd[(t * SK_WAVES + w) * 256 + tid];
         sum[t] = v;
@@ -1285,24 +1283,21 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         float* sq = &red[0][0][0];  // [MT][8 columns][16 rows] (red is not the reduction's)
         static_assert(MT * 8 * 16 <= SK_WAVES * 4 * 64, "squares fit the staging buffer");
         __builtin_amdgcn_s_waitcnt(0x0f70);  // (the prefetched values: landed long ago)
+        asm volatile("" : "+v"(rv), "+v"(wnv));
+        if (tid < 128 * MT) {
+            float se = 0.0f;
 #pragma unroll
-        for (int t = 0; t < MT; t++) asm volatile("" : "+v"(rv[t]));
-        asm volatile("" : "+v"(wnv));
-        if (tid < 256 && l < 32) {
-#pragma unroll
-            for (int t = 0; t < MT; t++) {
-                const int j = 4 * (l >> 4) + r, n = n0 + j, m = 16 * t + (l & 15);
-                float nv = 0.0f;
-                if (m < M && n < N) {
-                    float* o = reinterpret_cast<float*>(C) + (size_t)m * N + n;
-                    nv = rv[t] + sum[t];
-                    *o = nv;
-                    float yv = nv * h2f((u16)wnv);
-                    asm volatile("" : "+v"(yv));  // rounded to f32, then to f16 (no fused multiply-convert)
-                    np.y[(size_t)m * N + n] = f2h(yv);
-                }
-                sq[(t * 8 + j) * 16 + (l & 15)] = nv * nv;
+            for (int w = 0; w < SK_WAVES; w++) se += rd[((et * SK_WAVES + w) * 4 + er) * 64 + el];
+            const int n = n0 + ej;
+            float nv = 0.0f;
+            if (em < M && n < N) {
+                nv = rv + se;
+                reinterpret_cast<float*>(C)[(size_t)em * N + n] = nv;
+                float yv = nv * h2f((u16)wnv);
+                asm volatile("" : "+v"(yv));  // rounded to f32, then to f16 (no fused multiply-convert)
+                np.y[(size_t)em * N + n] = f2h(yv);
             }
+            sq[(et * 8 + ej) * 16 + (el & 15)] = nv * nv;
         }
         __syncthreads();
         if (tid < 16 * MT) {
