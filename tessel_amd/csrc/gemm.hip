@@ -1076,7 +1076,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
 #pragma unroll
         for (int t = 0; t < MT; t++) {
             const int m = 16 * t + (lane & 15);
-            rpos[t] = tid < 256 && m < M ? ep.pos[m] : -1;
+            rpos[t] = m < M ? ep.pos[m] : -1;
         }
         if (tid < 2 * M) rslot = ep.slot[tid >> 1];  // the write-out's row
     }
@@ -1090,7 +1090,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     // of row tile t = tid / 128: column n0 + 4 (l / 16) + r, row 16 t + l % 16.
     // Written out like the stream's loads; threads without an element read
     // column n0 of row 0.
-    const int et = tid >> 7, er = (tid & 127) >> 5, el = tid & 31;  // (R8)
+    const int et = tid >> 7, er = (tid & 127) >> 5, el = tid & 31;  // (R8; the rotary epilogue too)
     const int ej = 4 * (el >> 4) + er, em = 16 * et + (el & 15);
     float rv = 0.0f;
     uint32_t wnv = 0;
@@ -1197,12 +1197,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
         }
         if (u + XD < mysteps) load_x(st + SK_WAVES * XD, slot);
     }
-    float rc[ROPE ? MT : 1], rsn[ROPE ? MT : 1];
-    if constexpr (ROPE) {
-        const int n = n0 + 4 * ((tid & 63) >> 4) + (tid >> 6);
-#pragma unroll
-        for (int t = 0; t < MT; t++) rope_cs(ep, rpos[t], n, rc[t], rsn[t]);
-    }
     // Sum the 8 partial tiles through LDS in wavefront order; thread tid < 256
     // keeps element tid (register tid/64 of lane tid%64) of each. All MT
     // tiles go at once into the W block's LDS, free once every wavefront's
@@ -1221,7 +1215,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
 #pragma unroll
     for (int t = 0; t < MT; t++) {
         float v = 0.0f;
-        if (!R8 && tid < 256)  // (R8 sums its own element below)
+        if (!R8 && !ROPE && tid < 256)  // (R8 and the rotary epilogue sum their own elements below)
 #pragma unroll
             for (int w = 0; w < SK_WAVES; w++) v += rd[(t * SK_WAVES + w) * 256 + tid];
         sum[t] = v;
@@ -1231,7 +1225,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     // sit 32 lanes on: exchanged through LDS.
     const int r = tid >> 6, l = tid & 63;
     float up[MT];
-    if constexpr (DUAL) {
+    if constexpr (DUAL && !ROPE) {
 #pragma unroll
         for (int t = 0; t < MT; t++)
             if (tid < 256) xc[t * 256 + tid] = sum[t];
@@ -1239,36 +1233,40 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
 #pragma unroll
         for (int t = 0; t < MT; t++) up[t] = tid < 256 && l < 32 ? xc[t * 256 + r * 64 + l + 32] : 0.0f;
     }
-    if constexpr (RS) {
-        // rs[m] (the ring is free: every wavefront is past the reduction's
-        // barriers), then the sums of row m scaled by it.
-        ssv_fence(ssv);
-        float* rsb = reinterpret_cast<float*>(lds + WB / 2);  // [512] sums, then [32] rs
-        rs_from_partials(ssv, np.nr, M, K, np.eps, rsb, rsb + 512);
-#pragma unroll
-        for (int t = 0; t < MT; t++) {
-            const int m = 16 * t + (l & 15);
-            const float f = m < M ? rsb[512 + m] : 0.0f;
-            sum[t] *= f;
-            up[t] *= f;
-        }
-    }
     if constexpr (ROPE) {
+        // One pair per thread tid < 128 MT (the R8 epilogue's element
+        // mapping: pair ej of row em), both halves summed from the reduction
+        // buffer (the partner sits 32 lanes on), scaled by rs[em] (RS; the
+        // ring is free: every wavefront is past the reduction's barriers).
         // The block's 8 pairs lie in one head (D2 % 8 == 0): the rotated
         // halves go through LDS, then each token row leaves as two 16-byte
         // stores (per element 2-byte stores would scatter over 16 rows).
+        float f = 1.0f;
+        if constexpr (RS) {
+            ssv_fence(ssv);
+            float* rsb = reinterpret_cast<float*>(lds + WB / 2);  // [512] sums, then [32] rs
+            rs_from_partials(ssv, np.nr, M, K, np.eps, rsb, rsb + 512);
+            f = em < M ? rsb[512 + em] : 0.0f;
+        }
         static_assert(16 * MT * 16 * 2 <= (int)sizeof(red), "staging fits the reduction buffer");
         u16 (*yb)[16] = reinterpret_cast<u16 (*)[16]>(&red[0][0][0]);  // [16 MT][16] (red is not the reduction's)
-        if (tid < 256 && l < 32) {
+        if (tid < 128 * MT && em < M && n0 + ej < N) {
+            float v1 = 0.0f, v2 = 0.0f;
 #pragma unroll
-            for (int t = 0; t < MT; t++) {
-                const int pl = 4 * (l >> 4) + r, m = 16 * t + (l & 15);
-                if (m >= M || n0 + pl >= N) continue;
-                u16 y1, y2;
-                rope_pair(ep, n0 + pl, sum[t], up[t], rc[t], rsn[t], y1, y2);
-                yb[m][pl] = y1;
-                yb[m][8 + pl] = y2;
+            for (int w = 0; w < SK_WAVES; w++) {
+                const float* e = rd + ((et * SK_WAVES + w) * 4 + er) * 64 + el;
+                v1 += e[0];
+                v2 += e[32];
             }
+            int p = rpos[0];
+#pragma unroll
+            for (int t = 1; t < MT; t++) p = et == t ? rpos[t] : p;
+            float c, sn;
+            rope_cs(ep, p, n0 + ej, c, sn);
+            u16 y1, y2;
+            rope_pair(ep, n0 + ej, v1 * f, v2 * f, c, sn, y1, y2);
+            yb[em][ej] = y1;
+            yb[em][8 + ej] = y2;
         }
         __syncthreads();
         const int h = n0 / ep.D2, i0 = n0 % ep.D2;
