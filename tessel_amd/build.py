@@ -78,5 +78,32 @@ def build_sanitized():
     return out
 
 
+def build_poisoned():
+    """tessel_amd/libtessel_hip_poison.so: the GPU sources built with
+    -DTSL_POISON_LDS (every kernel fills its LDS with NaN words before it
+    starts, so a read of LDS nothing wrote shows up in the outputs), linked
+    with the normal host objects. On a GPU:
+
+        TSL_LIB=tessel_amd/libtessel_hip_poison.so python -m pytest tests -m gpu
+    """
+    build()
+    jobs, objs = [], []
+    for s in SOURCES:
+        o = os.path.join(BUILD, s.replace(".hip", ".poison.o"))
+        objs.append(o)
+        jobs.append([HIPCC] + HIP_FLAGS + ["-DTSL_POISON_LDS", "-c", os.path.join(CSRC, s), "-o", o])
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+        list(ex.map(_compile, jobs))
+    objs += [os.path.join(BUILD, s.replace(".cpp", ".o")) for s in HOST_SOURCES]
+    out = os.path.join(HERE, "libtessel_hip_poison.so")
+    _compile([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", out] + objs)
+    return out
+
+
 if __name__ == "__main__":
-    print(build_sanitized() if "--sanitize" in sys.argv else build(verbose=True))
+    if "--sanitize" in sys.argv:
+        print(build_sanitized())
+    elif "--poison" in sys.argv:
+        print(build_poisoned())
+    else:
+        print(build(verbose=True))

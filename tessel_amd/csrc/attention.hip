@@ -90,6 +90,7 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
     constexpr int NF = 2 + 16 * (DP / 32);  // floats per lane of a merged state: mc, lsum, acc
     constexpr int LDSB = KS * 2 * STAGE > 4 * NF * 64 * 4 || KS == 1 ? KS * 2 * STAGE : 4 * NF * 64 * 4;
     __shared__ __attribute__((aligned(16))) char lds[LDSB];  // [ks][stage]; at the end, the merge
+    TSL_POISON(lds);
 
     const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -21,6 +21,24 @@ typedef uint16_t u16;
 
 #define TSL_DEV __device__ __forceinline__
 
+// LDS poisoning for a debug build (hipcc -DTSL_POISON_LDS; build.py --poison):
+// at the start of a kernel every thread of the workgroup fills its LDS arrays
+// with all-ones words (NaN as f32 and as each f16 half), then a barrier, so a
+// read of LDS that nothing wrote shows up as NaN in the outputs (what the
+// reference's emulator does with its shared memory). Off in normal builds.
+#ifdef TSL_POISON_LDS
+#define TSL_POISON(arr) tsl_poison_lds(&(arr), sizeof(arr))
+__device__ inline void tsl_poison_lds(void* p, unsigned bytes) {
+    uint32_t* w = static_cast<uint32_t*>(p);
+    const unsigned nt = blockDim.x * blockDim.y * blockDim.z;
+    const unsigned t = threadIdx.x + blockDim.x * (threadIdx.y + blockDim.y * threadIdx.z);
+    for (unsigned i = t; i < bytes / 4; i += nt) w[i] = 0xffffffffu;
+    __syncthreads();
+}
+#else
+#define TSL_POISON(arr) ((void)0)
+#endif
+
 // Reinterpreting one element of an ext_vector in place,
 // __builtin_bit_cast(T, v[i]), reads element 0 whatever i is with this
 // clang (checked on the host: {1, 2, 3, 4}[i] as float gives 1 for every i).

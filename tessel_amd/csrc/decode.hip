@@ -63,6 +63,7 @@ __global__ __launch_bounds__(256) void decode_partial(DecArgs a) {
     constexpr int TPS = 4 * TPI;     // tokens per workgroup per step
     constexpr int U = 4;             // steps per softmax update
     __shared__ float red[4][QPG][2 + D];
+    TSL_POISON(red);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = blockIdx.x % a.NCH, bg = blockIdx.x / a.NCH;
@@ -288,6 +289,7 @@ __global__ __launch_bounds__(64 * NWV) void decode_tiles(DecArgs a) {
     constexpr float LAZY = 8.0f;
     static_assert(DEC_STAGES >= 2 && DEC_STAGES <= 4, "wait_tiles covers up to 3 tiles in flight");
     __shared__ __attribute__((aligned(16))) char lds[NWV * DEC_STAGES * WSTAGE];  // a ring per wavefront
+    TSL_POISON(lds);
 
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, col = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -603,6 +605,7 @@ __global__ __launch_bounds__(64 * NWV) void decode_stream(DecArgs a) {
     static_assert(LDS == NWV * STG * WSTAGE + NWV * 512 + (2 * DS_MAX_B + 1) * 4 && LDS <= 163840, "LDS");
     static_assert(2 * LPT + 2 <= 30, "ds_wait covers the loads in flight");
     __shared__ __attribute__((aligned(16))) char lds[LDS];
+    TSL_POISON(lds);
     int* wsl = reinterpret_cast<int*>(lds + NWV * STG * WSTAGE);  // [NWV][2][64] table windows
     int* pre = wsl + NWV * 128;                                   // [B + 1] first unit of b
     int* ln = pre + DS_MAX_B + 1;                                 // [B] lens

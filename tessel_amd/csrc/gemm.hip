@@ -90,6 +90,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_f16(const u16* __restri
     __shared__ u32x4 lds_a[2][BM * KC];
     __shared__ u32x4 lds_b[2][BN * KC];
     __shared__ u32x4 lds_b2[DUAL ? 2 : 1][DUAL ? BN * KC : 1];
+    TSL_POISON(lds_a); TSL_POISON(lds_b); TSL_POISON(lds_b2);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
@@ -340,6 +341,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     constexpr int STAGE = BM * BK * 2 + (DUAL ? 2 : 1) * BB;  // bytes per stage: A [BM][BK], then B (, B2)
     constexpr int LPS = LPA + (DUAL ? 2 : 1) * LPB;          // loads per wave per stage
     __shared__ __attribute__((aligned(16))) u16 lds[NS * STAGE / 2];
+    TSL_POISON(lds);
     // Row r of an A (W) tile holds logical 16-byte chunk c at c ^ sw(r).
     auto sw = [](int r) { return KC == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
 
@@ -590,6 +592,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, con
     constexpr int STAGE = NH * HALF;
     constexpr int SUB = 4 * NH;  // 16-k substeps per phase
     __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE / 2];
+    TSL_POISON(lds);
     auto sw = [](int r) { return (r >> 1) & 7; };
 
     const int lane = threadIdx.x & 63;
@@ -746,6 +749,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, con
 __global__ __launch_bounds__(256) void matmul_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                          float* __restrict__ C, int M, int N, int K) {
     __shared__ float As[16][64 + 1], Bs[16][64 + 1];
+    TSL_POISON(As); TSL_POISON(Bs);
     const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
     const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
     float acc[4][4] = {};
@@ -816,6 +820,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const u16* __restri
     constexpr int NW = DUAL ? 2 * RT : RT;  // W tiles per step (gate rows then up rows)
     constexpr int NACC = NW * MT;
     __shared__ float red[SK_WAVES][4][64];
+    TSL_POISON(red);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * 16 * RT;
     const int row = lane & 15, g = lane >> 4;
@@ -1058,6 +1063,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
     constexpr int XL = 2 * MT;                   // X loads per step (8 rows each)
     __shared__ __attribute__((aligned(16))) u16 lds[(WB + SK_WAVES * XD * XS) / 2];
     __shared__ __attribute__((aligned(16))) float red[SK_WAVES][4][64];
+    TSL_POISON(lds); TSL_POISON(red);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row = lane & 15, g = lane >> 4;
@@ -1355,6 +1361,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_pst(const u16* __re
     __shared__ float red[MT][SK_WAVES][4][64];
     __shared__ float xch[DUAL ? MT : 1][4][64];
     __shared__ float rsl[RS ? 512 + 32 : 1];
+    TSL_POISON(lds); TSL_POISON(red); TSL_POISON(xch); TSL_POISON(rsl);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row = lane & 15, g = lane >> 4;
@@ -1881,6 +1888,7 @@ bool qkv_fused(TslKernel& k) {
 __global__ __launch_bounds__(256) void rows_rs_kernel(const u16* __restrict__ Y, const float* __restrict__ SS,
                                                       u16* __restrict__ H, int M, int K, int NB, float eps) {
     __shared__ float pr[16];
+    TSL_POISON(pr);
     const int m = blockIdx.x, t = threadIdx.x;
     if (t < 16) {
         float a = 0.0f;

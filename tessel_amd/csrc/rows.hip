@@ -233,6 +233,7 @@ __global__ __launch_bounds__(256) void rmsnorm_wg_kernel(const float* __restrict
                                                          int xrows, const u16* __restrict__ W, u16* __restrict__ Y,
                                                          int C, int ncols, float n, float eps) {
     __shared__ float red[4];
+    TSL_POISON(red);
     const int t = threadIdx.x, row = blockIdx.x;
     const int src = idx ? idx[row] : row;
     const bool rin = src >= 0 && src < xrows;
@@ -263,6 +264,7 @@ __global__ __launch_bounds__(256) void reduce_rmsnorm_kernel(const float* __rest
                                                              float* __restrict__ R, const u16* __restrict__ W,
                                                              u16* __restrict__ Y, int M, int C, float n, float eps) {
     __shared__ float red[4];
+    TSL_POISON(red);
     const int t = threadIdx.x, row = blockIdx.x;
     const size_t mc = (size_t)M * C;
     float* r = R + (size_t)row * C;
@@ -560,6 +562,7 @@ __global__ __launch_bounds__(AM_THREADS) void argmax_kernel(const float* __restr
     constexpr int NW = AM_THREADS / 64;
     __shared__ float rv[NW];
     __shared__ int ri[NW];
+    TSL_POISON(rv); TSL_POISON(ri);
     const int tid = threadIdx.x;
     const float* x = X + (size_t)blockIdx.x * V;
     float bv = 0.0f;
