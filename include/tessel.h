@@ -193,6 +193,13 @@ int tsl_engine_profile_rows(int engine, char* out, size_t cap, size_t* len);
  * into rows/graphs, *n the number recorded. */
 int tsl_engine_graphs(int engine, int32_t* rows, int32_t* graphs, int cap, int* n);
 
+/* No counterpart in the reference (the reference normalises before every
+ * projection): decode steps of up to 32 rows defer each rmsnorm into the
+ * consuming projection, through Y = f16(R Wn), which overflows f16 where
+ * |R Wn| >= 65520 although rmsnorm(R) Wn need not. Such a step is recomputed
+ * with every norm applied first; *n gets how many steps were. */
+int tsl_engine_fallbacks(int engine, int64_t* n);
+
 /* Engine::step (src/llm/engine.rs:275-354). mode 0 = Prefill, 1 = Packed
  * (starts[n]), 2 = Decode (tables: nseq rows of max_seq_pages pages, lens:
  * nseq). logits receives nwant * vocab floats for rows want[0..nwant). */

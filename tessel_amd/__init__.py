@@ -51,7 +51,7 @@ EXPORTS = [
     "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
     "tsl_checkpoint_save", "tsl_json_roundtrip", "tsl_rng_new", "tsl_rng_bits", "tsl_rng_tensor",
     "tsl_time_each", "tsl_engine_profile", "tsl_engine_profile_rows", "tsl_schedule_trace",
-    "tsl_graph_nodes", "tsl_engine_graphs", "tsl_probe_mfma", "tsl_probe_stream",
+    "tsl_graph_nodes", "tsl_engine_graphs", "tsl_engine_fallbacks", "tsl_probe_mfma", "tsl_probe_stream",
     "tsl_decode_attention_noalloc",
 ]
 
@@ -121,6 +121,7 @@ def _declare(L):
     L.tsl_probe_mfma.argtypes = [_INT, _INT, _INT, ctypes.POINTER(ctypes.c_double)]
     L.tsl_probe_stream.argtypes = [_U64, ctypes.c_size_t, ctypes.c_size_t, _INT, ctypes.POINTER(ctypes.c_double)]
     L.tsl_engine_graphs.argtypes = [_INT, _P, _P, _INT, ctypes.POINTER(_INT)]
+    L.tsl_engine_fallbacks.argtypes = [_INT, ctypes.POINTER(_I64)]
     L.tsl_decode_attention_noalloc.argtypes = [_U64] * 6 + [ctypes.c_float] + [_INT] * 7
     L.tsl_schedule_trace.argtypes = [ctypes.POINTER(Limits), _INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, _P,
                                      ctypes.POINTER(Stats), _P, _I64, ctypes.POINTER(_I64)]
@@ -485,6 +486,13 @@ class Engine:
         rows, ids, n = np.zeros(64, np.int32), np.zeros(64, np.int32), _INT()
         check(lib().tsl_engine_graphs(self.handle, rows.ctypes.data, ids.ctypes.data, 64, ctypes.byref(n)))
         return dict(zip(rows[:n.value].tolist(), ids[:n.value].tolist()))
+
+    def fallbacks(self):
+        """Decode steps recomputed with every rmsnorm applied first, because
+        the deferred form's Y = f16(R Wn) overflowed."""
+        n = _I64()
+        check(lib().tsl_engine_fallbacks(self.handle, ctypes.byref(n)))
+        return n.value
 
     def profile(self, on):
         """Gpu::profile: time every launch on its own (graphs off) from now."""

@@ -238,9 +238,30 @@ def warm_up():
     _free(bufs)
 
 
+# Meta values the launchers read (rows.hip / gemm.hip: the column chunk of
+# the row kernels). Tiles, stages and wavefronts are chosen from the shape, so
+# BM/BN/BK/BR and the warp count enter only a kernel's cache key.
+CODE_META = ("BC",)
+
+
+def distinct_configs(configs):
+    """The candidates of a case that run different code: one per distinct
+    value of the meta the launchers read (CODE_META), the first of each."""
+    seen, keep = set(), []
+    for meta, warps in configs:
+        code = tuple((k, v) for k, v in meta if k in CODE_META)
+        if code not in seen:
+            seen.add(code)
+            keep.append((meta, warps))
+    return keep
+
+
 def bench(quick, iters, tuned, out):
     """bench::run (src/bench.rs:292-407): tunes (or takes the configuration
-    tuned before, from `tuned`) and times every case; one JSON line each."""
+    tuned before, from `tuned`) and times every case; one JSON line each.
+    The reference times every tile configuration; here the tiles follow from
+    the shape, so only candidates that run different code (distinct_configs)
+    are timed, and the line says so ("tiles": "by shape")."""
     T.open()
     device = T.device_name()
     cache = {}
@@ -257,7 +278,7 @@ def bench(quick, iters, tuned, out):
         tried = []
         best = None
         bufs = None
-        for meta, warps in case.configs:
+        for meta, warps in distinct_configs(case.configs):
             name = config_name(meta, warps)
             if chosen is not None and chosen != name:
                 continue
@@ -294,7 +315,7 @@ def bench(quick, iters, tuned, out):
         out(f'{{"kind": {json_str(case.kind)}, "label": {json_str(case.label)}, "engine": "tessel", '
             f'"device": {json_str(device)}, "median_ms": {med:.4f}, "min_ms": {mn:.4f}, "tflops": {tflops:.3f}, '
             f'"gbps": {gbps:.1f}, "rel_err": {rust_e(err, 3)}, "sm_mhz": null, "config": {json_str(name)}, '
-            f'"tried": [{", ".join(tried)}]}}')
+            f'"tiles": "by shape", "tried": [{", ".join(tried)}]}}')
 
 
 # ---------------------------------------------------------------- llm (src/main.rs:199-318)

@@ -131,6 +131,13 @@ struct Engine {
     Buf embed, head, norm, cos, sin;
     std::vector<Layer> layers;
     Buf x, h, ss, qkv, q, k, v, o, mlp, last, logits, tok, pos, slot, idx, table, lens, starts, next;
+    // outw: the deferred-norm overflow flag (word 0), then at byte 16 the
+    // step's token ids (next), so one download returns both.
+    Buf outw, ovf;
+    // Set while a step is recomputed with every rmsnorm applied before its
+    // projection (after the deferred form overflowed f16).
+    bool plain = false;
+    int64_t prenorm_fallbacks = 0;
     // One device arena for a step's inputs, filled by one upload: for a step
     // of t (padded) rows, tok, pos, slot, idx, starts, lens (t ints each),
     // then table (t max_seq_pages ints). layout(t) points the buffers there;
@@ -287,9 +294,17 @@ struct Engine {
         TRY(alloc(t * d * 2, last));
         TRY(alloc(t * (size_t)cfg.vocab * 4, logits));
         TRY(alloc(t * (6 + (size_t)lim.max_seq_pages) * 4, in));
-        TRY(alloc(t * 4, next));
+        TRY(alloc(16 + t * 4, outw));
+        ovf = Buf{outw.p, 4};
+        next = Buf{outw.p + 16, t * 4};
+        const int32_t zero = 0;
+        TRY(write(ovf, 0, &zero, 4));
         return 0;
     }
+
+    // Decode steps of up to 32 rows defer each rmsnorm into the projection
+    // that consumes it (launch_all), unless the step is being recomputed.
+    bool uses_prenorm(size_t t, bool prefill) const { return !prefill && t <= 32 && !plain; }
 
     // Engine::launch_all (src/llm/engine.rs:359-529).
     int launch_all(size_t t, bool prefill, size_t bw) {
@@ -341,13 +356,13 @@ struct Engine {
         // and gate_up / the next layer's QKV scale their rows by 1 / rms
         // (fused/gate_up_rs, fused/qkv_rs_rope_kv): no normalisation launch
         // between the two, and no second pass over R.
-        const bool prenorm = !prefill && T <= 32;
+        const bool prenorm = uses_prenorm(t, prefill);
         const int64_t nb8 = (dm + 7) / 8;
         int o_pre_k = -1, down_pre_k = -1, gu_rs_k = -1, qkv_rs_k = -1;
         if (prenorm) {
-            TRY(kernel("linear_residual_prenorm", {{T, nh * hd}, {dm, nh * hd}, {T, dm}, {dm}, {T, dm}, {nb8, T}}, {}, 4,
-                       &o_pre_k, "fused"));
-            TRY(kernel("linear_residual_prenorm", {{T, f}, {dm, f}, {T, dm}, {dm}, {T, dm}, {nb8, T}}, {}, 4,
+            TRY(kernel("linear_residual_prenorm", {{T, nh * hd}, {dm, nh * hd}, {T, dm}, {dm}, {T, dm}, {nb8, T}, {1}},
+                       {}, 4, &o_pre_k, "fused"));
+            TRY(kernel("linear_residual_prenorm", {{T, f}, {dm, f}, {T, dm}, {dm}, {T, dm}, {nb8, T}, {1}}, {}, 4,
                        &down_pre_k, "fused"));
             TRY(kernel("gate_up_rs", {{T, dm}, {nb8, T}, {f, dm}, {f, dm}, {T, f}}, {}, 4, &gu_rs_k, "fused"));
             TRY(kernel("qkv_rs_rope_kv",
@@ -369,14 +384,14 @@ struct Engine {
             if (prefill) TRY(launch(att_k, {B(q), B(k), B(v), B(starts), B(o), SC}));
             else TRY(launch(att_k, {B(q), B(L.kc), B(L.vc), B(table), B(lens), B(o), SC}));
             if (prenorm) {
-                TRY(launch(o_pre_k, {B(o), B(L.wo), B(x), B(L.n2), B(h), B(ss)}));
+                TRY(launch(o_pre_k, {B(o), B(L.wo), B(x), B(L.n2), B(h), B(ss), B(ovf)}));
                 TRY(launch(gu_rs_k, {B(h), B(ss), B(L.wg), B(L.wu), B(mlp), EPS}));
             } else {
                 TRY(launch(oproj_norm_k, {B(o), B(L.wo), B(x), B(L.n2), B(h), EPS}));
                 TRY(launch(gu_k, {B(h), B(L.wg), B(L.wu), B(mlp)}));
             }
             if (li + 1 < layers.size()) {
-                if (prenorm) TRY(launch(down_pre_k, {B(mlp), B(L.wd), B(x), B(layers[li + 1].n1), B(h), B(ss)}));
+                if (prenorm) TRY(launch(down_pre_k, {B(mlp), B(L.wd), B(x), B(layers[li + 1].n1), B(h), B(ss), B(ovf)}));
                 else TRY(launch(down_norm_k, {B(mlp), B(L.wd), B(x), B(layers[li + 1].n1), B(h), EPS}));
             } else {
                 TRY(launch(down_k, {B(mlp), B(L.wd), B(x)}));
@@ -414,9 +429,9 @@ struct Engine {
         if (mode == PACKED && !st_in) return tsl_fail(TSL_ERR_ARG, "packed prefill: one start per token");
         if (mode == PACKED)  // each row's sequence starts at or before it, and sequences do not overlap
             for (size_t i = 0; i < n; i++)
-                if (st_in[i] < 0 || (size_t)st_in[i] > i || (i > 0 && st_in[i] < st_in[i - 1]))
-                    return tsl_fail(TSL_ERR_ARG, "packed prefill: starts must satisfy 0 <= starts[i] <= i, "
-                                                 "non-decreasing");
+                if (i == 0 ? st_in[0] != 0 : (st_in[i] != st_in[i - 1] && (size_t)st_in[i] != i))
+                    return tsl_fail(TSL_ERR_ARG, "packed prefill: starts[0] must be 0 and each starts[i] "
+                                                 "starts[i - 1] (same sequence) or i (a new one)");
         if (mode == DECODE && nseq > t) return tsl_fail(TSL_ERR_ARG, "decode: more sequences than rows");
         if (bw > t) return tsl_fail(TSL_ERR_ARG, "more logits rows than step rows");
         // Every input of the step in the arena's layout for t, one upload.
@@ -462,10 +477,37 @@ struct Engine {
         } else {
             TRY(launch_all(t, prefill, bw));
         }
+        if (uses_prenorm(t, prefill)) {
+            // The deferred norms leave Y = f16(R Wn), which overflows where
+            // |R Wn| >= 65520 although the normalised rows need not: such a
+            // step is recomputed with each norm applied first, as prefill
+            // steps do (the step's KV writes are the same slots, rewritten).
+            int32_t flag = 0;
+            if (out_tok && nwant) {
+                dl.resize(4 + nwant);
+                TRY(tsl_download(dl.data(), outw.p, 16 + nwant * 4));
+                flag = dl[0];
+            } else {
+                TRY(tsl_download(&flag, ovf.p, 4));
+            }
+            if (flag) {
+                prenorm_fallbacks++;
+                const int32_t zero = 0;
+                TRY(write(ovf, 0, &zero, 4));
+                plain = true;
+                const int r = launch_all(t, false, bw);
+                plain = false;
+                TRY(r);
+            } else if (out_tok && nwant) {
+                std::copy(dl.begin() + 4, dl.end(), out_tok);
+                return 0;
+            }
+        }
         if (nwant == 0) return 0;
         if (out_tok) return tsl_download(out_tok, next.p, nwant * 4);
         return tsl_download(out, logits.p, nwant * (size_t)cfg.vocab * 4);
     }
+    std::vector<int32_t> dl;
 };
 
 std::vector<std::unique_ptr<Engine>> g_engines;
@@ -566,7 +608,7 @@ int tsl_engine_free(int engine) {
     tsl_sync();
     // (tok, pos, slot, idx, starts, lens and table are views into `in`.)
     Buf* bufs[] = {&e->embed, &e->norm, &e->cos, &e->sin, &e->x, &e->h, &e->ss, &e->qkv, &e->q, &e->k, &e->v,
-                   &e->o, &e->mlp, &e->last, &e->logits, &e->in, &e->next};
+                   &e->o, &e->mlp, &e->last, &e->logits, &e->in, &e->outw};
     if (e->head.p != e->embed.p) tsl_free(e->head.p);
     for (Buf* b : bufs)
         if (b->p) tsl_free(b->p);
@@ -623,6 +665,13 @@ int tsl_engine_graphs(int engine, int32_t* rows, int32_t* graphs, int cap, int* 
         i++;
     }
     *n = i;
+    return 0;
+}
+
+int tsl_engine_fallbacks(int engine, int64_t* n) {
+    Engine* e = get(engine);
+    if (!e || !n) return tsl_fail(TSL_ERR_ARG, "no such engine, or a null count");
+    *n = e->prenorm_fallbacks;
     return 0;
 }
 
@@ -688,6 +737,8 @@ int schedule(const Sched& sc, int nreq, const int32_t* prompts, const int64_t* o
     const int p = sc.lim.page;
     const size_t mp = sc.lim.max_seq_pages;
     if (nreq < 0 || max_batch < 1 || p < 1) return tsl_fail(TSL_ERR_ARG, "generate: bad request count or batch");
+    if (nreq > 0 && (!prompts || !offsets || !max_new || !out_tokens || !out_counts))
+        return tsl_fail(TSL_ERR_ARG, "generate: null prompts, offsets, max_new or outputs");
     for (int id = 0; id < nreq; id++) {
         int64_t plen = offsets[id + 1] - offsets[id];
         std::ostringstream m;
@@ -851,6 +902,9 @@ int tsl_schedule_trace(const tsl_limits* lim, int eos, int nreq, const int32_t* 
                        const int32_t* max_new, int max_batch, int packed, const int32_t* script, int32_t* out_tokens,
                        int32_t* out_counts, tsl_stats* stats, int32_t* trace, int64_t cap, int64_t* used) {
     if (!lim || !trace || !used || cap < 0) return tsl_fail(TSL_ERR_ARG, "schedule trace: null argument");
+    if (nreq < 0) return tsl_fail(TSL_ERR_ARG, "schedule trace: negative request count");
+    if (nreq > 0 && (!prompts || !offsets || !max_new || !script || !out_tokens || !out_counts))
+        return tsl_fail(TSL_ERR_ARG, "schedule trace: null prompts, offsets, max_new, script or outputs");
     std::vector<size_t> base(nreq > 0 ? nreq : 0, 0);
     for (int i = 1; i < nreq; i++) base[i] = base[i - 1] + (max_new[i - 1] > 0 ? max_new[i - 1] : 0);
     std::vector<int> emitted(base.size(), 0);

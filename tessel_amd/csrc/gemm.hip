@@ -986,6 +986,7 @@ constexpr int sl_xdepth() { return MT <= 2 ? 2 : 1; }
 struct NormPre {
     const u16* w = nullptr;  // producer: Wn [N]
     u16* y = nullptr;        // producer: Y [M, N]
+    int* ovf = nullptr;      // producer: set to 1 when some Y overflows f16
     const float* ss = nullptr;  // consumer: [nr, M]
     int nr = 0;
     float eps = 0.0f;
@@ -1299,7 +1300,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
                 reinterpret_cast<float*>(C)[(size_t)em * N + n] = nv;
                 float yv = nv * h2f((u16)wnv);
                 asm volatile("" : "+v"(yv));  // rounded to f32, then to f16 (no fused multiply-convert)
-                np.y[(size_t)em * N + n] = f2h(yv);
+                const u16 yh = f2h(yv);
+                np.y[(size_t)em * N + n] = yh;
+                if ((yh & 0x7c00) == 0x7c00) *np.ovf = 1;  // inf or NaN: the caller normalises first instead
             }
             sq[(et * 8 + ej) * 16 + (el & 15)] = nv * nv;
         }
@@ -1905,8 +1908,8 @@ __global__ __launch_bounds__(256) void rows_rs_kernel(const u16* __restrict__ Y,
 // The prenorm producer's fallback: Y = f16(R Wn) and the per-8-column sums
 // of squares, as the fused kernel computes them.
 __global__ __launch_bounds__(256) void prenorm_kernel(const float* __restrict__ R, const u16* __restrict__ Wn,
-                                                      u16* __restrict__ Y, float* __restrict__ SS, int M, int N,
-                                                      int NB) {
+                                                      u16* __restrict__ Y, float* __restrict__ SS, int* ovf, int M,
+                                                      int N, int NB) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     if (i >= (long)NB * M) return;
     const int b = (int)(i / M), m = (int)(i % M);
@@ -1917,7 +1920,9 @@ __global__ __launch_bounds__(256) void prenorm_kernel(const float* __restrict__ 
         const float v = R[(size_t)m * N + n];
         float yv = v * h2f(Wn[n]);
         asm volatile("" : "+v"(yv));  // rounded to f32, then to f16 (as the fused kernel)
-        Y[(size_t)m * N + n] = f2h(yv);
+        const u16 yh = f2h(yv);
+        Y[(size_t)m * N + n] = yh;
+        if ((yh & 0x7c00) == 0x7c00) *ovf = 1;
         float q = v * v;
         asm volatile("" : "+v"(q));  // the product rounded, not contracted into an fma (as in the fused kernel)
         a += q;
@@ -1934,7 +1939,10 @@ int launch_qkv_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
 // llm/linear_residual, R += X W^T, leaving for the next projection's rmsnorm
 // Y = f16(R Wn) and SS[b][m], the sum over the 8 columns n = 8 b .. 8 b + 7
 // (column order) of the new R[m][n]^2. Arguments X [M, K], W [N, K], R [M, N],
-// Wn [N], Y [M, N], SS [NB, M], NB = ceil(N / 8).
+// Wn [N], Y [M, N], SS [NB, M], NB = ceil(N / 8), OVF [1]. Y overflows f16
+// where |R Wn| >= 65520 although rmsnorm(R) Wn may not: then the kernel sets
+// OVF[0] = 1 (it never clears it) and the caller should normalise first
+// (fused/linear_residual_rmsnorm), as the engine does.
 int launch_linear_residual_prenorm(TslKernel& k, const uint64_t* a, hipStream_t s) {
     const int M = k.dim("M"), N = k.dim("N"), K = k.dim("K"), NB = k.dim("NB");
     if (NB != (N + 7) / 8) return tsl_fail(-2, "linear_residual_prenorm: NB must be ceil(N / 8)");
@@ -1944,6 +1952,7 @@ int launch_linear_residual_prenorm(TslKernel& k, const uint64_t* a, hipStream_t 
     NormPre np;
     np.w = P<u16>(a[3]), np.y = P<u16>(a[4]);
     float* SS = P<float>(a[5]);
+    np.ovf = P<int>(a[6]);
     if (M <= 64 && K % 128 == 0 && K > 0 && K <= 2 * SL_KS) {
         auto go = [&](auto mt) {
             hipLaunchKernelGGL((gemm_skinny_lds<EPI_RESID, decltype(mt)::value, false, true>), dim3(NB),
@@ -1960,7 +1969,7 @@ int launch_linear_residual_prenorm(TslKernel& k, const uint64_t* a, hipStream_t 
     if (int e = gemm_dispatch<true, EPI_RESID>(X, W, nullptr, R, nullptr, M, N, K, s, "linear_residual_prenorm", nullptr))
         return e;
     const long n = (long)NB * M;
-    hipLaunchKernelGGL(prenorm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, R, np.w, np.y, SS, M, N, NB);
+    hipLaunchKernelGGL(prenorm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, R, np.w, np.y, SS, np.ovf, M, N, NB);
     return TSL_LAUNCHED("linear_residual_prenorm");
 }
 
@@ -1995,7 +2004,7 @@ int launch_gate_up_rs(TslKernel& k, const uint64_t* a, hipStream_t s) {
 }
 int prepare_gate_up_rs(TslKernel& k) {
     const int64_t M = k.dim("M"), F = k.dim("F"), K = k.dim("K"), NB = k.dim("NB");
-    if (NB < 1) return tsl_fail(-2, "gate_up_rs: NB must be at least 1");
+    if (NB != (K + 7) / 8) return tsl_fail(-2, "gate_up_rs: NB must be ceil(K / 8)");
     if (M > (1 << 20) || K > (1 << 20) || rs_pst_fits((int)M, (int)F, (int)K, (int)NB)) return 0;
     const size_t bytes = (size_t)M * K * 2;
     if (bytes == 0) return 0;
@@ -2021,7 +2030,7 @@ int launch_qkv_rs_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
     return qkv_rope_kv_run(k, a, s, H, nullptr, NormPre{});
 }
 int prepare_qkv_rs_rope_kv(TslKernel& k) {
-    if (k.dim("NB") < 1) return tsl_fail(-2, "qkv_rs_rope_kv: NB must be at least 1");
+    if (k.dim("NB") != (k.dim("Dm") + 7) / 8) return tsl_fail(-2, "qkv_rs_rope_kv: NB must be ceil(Dm / 8)");
     if (qkv_rs_fits(k)) return 0;
     const size_t bytes = (size_t)k.dim("T") * k.dim("Dm") * 2;
     if (bytes == 0) return 0;

@@ -156,7 +156,7 @@ std::vector<KernelDef> g_defs = {
     // deferred, as Y = f16(R Wn) and per-8-column sums of squares of R (the
     // engine's fusion; its consumers are gate_up_rs and qkv_rs_rope_kv).
     {"fused", "linear_residual_prenorm",
-     "X: f16[M, K], W: f16[N, K], R: f32[M, N], Wn: f16[N], Y: f16[M, N], SS: f32[NB, M]", "", "",
+     "X: f16[M, K], W: f16[N, K], R: f32[M, N], Wn: f16[N], Y: f16[M, N], SS: f32[NB, M], OVF: i32[1]", "", "",
      launch_linear_residual_prenorm, nullptr},
     // Not a .tl kernel: llm/gate_up of rmsnorm(R) Wn given as Y and SS (the
     // engine's fusion).

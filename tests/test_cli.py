@@ -78,7 +78,10 @@ def test_bench_quick_lines(tmp_path):
         assert set(x) >= {"kind", "label", "engine", "device", "median_ms", "min_ms", "tflops", "gbps", "rel_err",
                           "sm_mhz", "config", "tried"}
         assert x["rel_err"] < 2e-2 and x["median_ms"] > 0, x
-    assert rows[0]["label"] == "1024x1024x1024" and len(rows[0]["tried"]) == 2
+    # Tiles follow from the shape: one candidate per case runs distinct code,
+    # and only it is timed.
+    assert rows[0]["label"] == "1024x1024x1024"
+    assert all(len(x["tried"]) == 1 and x["tiles"] == "by shape" for x in rows)
     assert [json.loads(x) for x in out.read_text().splitlines()] == rows
     # The tuned file keeps the choice: a second run times only it.
     r = _cli("bench", "--quick", "--iters", "5", "--tuned", str(tuned))
@@ -116,3 +119,14 @@ def test_llm_on_a_tiny_checkpoint(tmp_path):
     assert line["outputs"] == outs
     logits = json.loads((tmp_path / "l.json").read_text())
     assert len(logits) == cfg.vocab
+
+
+def test_distinct_configs_keeps_one_per_code():
+    # Candidates differing only in tiles or warps run the same code (one is
+    # kept); a different column chunk (BC, read by the row kernels) is
+    # different code.
+    from tessel_amd.cli import distinct_configs
+    c = [([("BM", 64), ("BN", 64)], 4), ([("BM", 128), ("BN", 64)], 8)]
+    assert distinct_configs(c) == c[:1]
+    r = [([("BR", 1), ("BC", 1024)], 4), ([("BR", 2), ("BC", 1024)], 4), ([("BR", 1), ("BC", 2048)], 8)]
+    assert distinct_configs(r) == [r[0], r[2]]

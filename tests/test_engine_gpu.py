@@ -243,18 +243,66 @@ def test_tinyllama_full_config_properties(gpu):
 
 def test_engine_rejects_bad_requests_and_starts(gpu):
     # max_new 0 and a request larger than the page pool are refused before
-    # any step runs; packed starts must satisfy 0 <= starts[i] <= i and be
-    # non-decreasing (a start outside the rows would address K/V before or
-    # past the step).
+    # any step runs; packed starts must be 0 at row 0 and, at every later
+    # row, the previous row's start (same sequence) or the row itself (a new
+    # one): a start outside the rows would address K/V before or past the
+    # step.
     cfg = T.Config.tiny()
     e = T.Engine(cfg, limits(), T.weights_random(cfg, 3))
     with pytest.raises(RuntimeError, match="max_new must be at least 1"):
         e.generate([([1, 2, 3], 2), ([4, 5], 0)], 2)
     with pytest.raises(RuntimeError, match="does not fit"):
         T.Engine.generate(e, [([1] * 16, 300)], 1)
-    for bad in ([0, 0, -1, 3], [0, 0, 3, 3], [0, 1, 0, 3]):
+    # [0, 0, 1, 1]: row 2 claims a sequence starting at row 1, which belongs
+    # to the sequence that starts at row 0.
+    for bad in ([0, 0, -1, 3], [0, 0, 3, 3], [0, 1, 0, 3], [0, 0, 1, 1], [1, 1, 2, 3]):
         with pytest.raises(RuntimeError, match="starts"):
             e.step([1, 2, 3, 4], [0, 1, 0, 1], [0, 1, 2, 3], T.Engine.PACKED, starts=bad, want=[3])
     got = e.step([1, 2, 3, 4], [0, 1, 0, 1], [0, 1, 2, 3], T.Engine.PACKED, starts=[0, 0, 2, 2], want=[1, 3])
     assert np.isfinite(got).all()
     e.close()
+
+
+def test_deferred_norm_overflow_recomputes_the_step(gpu):
+    """Decode steps defer each rmsnorm into the next projection through
+    Y = f16(R Wn). With embeddings (the residual's start) up to 2000 and
+    norm weights of 40, R Wn overflows f16 (|R Wn| >= 65520) while
+    rmsnorm(R) Wn stays below ~70: the
+    engine must notice and recompute the step with the norms applied first,
+    so its tokens stay the reference's (src/llm/reference.rs normalises
+    first). Without the overflow no step is recomputed."""
+    cfg = T.Config.tiny()
+    emb, lay, nrm, head = T.weights_random(cfg, 13)
+    ocfg = oracle.Config.tiny()
+    prompt = [1, 17, 200, 33, 5]
+    for big in (False, True):
+        e_w = emb.copy()
+        l_w = lay.copy()
+        if big:
+            e_w = (e_w.astype(np.float32) * (2000 / np.abs(e_w.astype(np.float32)).max())).astype(np.float16)
+            per = l_w.size // cfg.layers
+            d, qr = cfg.dim, cfg.qkv() * cfg.dim
+            hd = cfg.heads * cfg.head_dim
+            for li in range(cfg.layers):  # every norm weight (attn_norm and mlp_norm) 40
+                b = li * per
+                l_w[b:b + d] = 40
+                n2 = b + d + qr + d * hd
+                l_w[n2:n2 + d] = 40
+        w = (e_w, l_w, nrm, head)
+        e = T.Engine(cfg, limits(), w)
+        outs, st = e.generate([(prompt, 6), ([4, 9, 100], 5)], 2)
+        fb = e.fallbacks()
+        e.close()
+        print(f"big={big}: {fb} of {st.decode_steps} decode steps recomputed", flush=True)
+        if not big:
+            assert fb == 0
+            continue
+        assert fb == st.decode_steps > 0
+        for p, toks in zip((prompt, [4, 9, 100]), outs):
+            seq = list(p)
+            for t in toks:
+                l = oracle.forward(ocfg, w, seq)[-1]
+                assert np.isfinite(l).all()
+                best = oracle.argmax(l)
+                assert t == best or l[best] - l[t] < 2e-2 * np.abs(l).max(), (t, best)
+                seq.append(t)

@@ -634,13 +634,37 @@ def _prenorm(r, m, ko, dm):
     wn = r.tensor("f16", [dm], 1.0)
     nb = (dm + 7) // 8
     out = T.run("fused", "linear_residual_prenorm",
-                [x, w, res.copy(), wn, np.zeros((m, dm), np.float16), np.zeros((nb, m), np.float32)], outputs=[2, 4, 5])
+                [x, w, res.copy(), wn, np.zeros((m, dm), np.float16), np.zeros((nb, m), np.float32),
+                 np.zeros(1, np.int32)], outputs=[2, 4, 5, 6])
+    assert out[6][0] == 0  # no overflow flagged
     want_r = oracle.linear_residual(x, w, res.copy())
     parity("prenorm R", out[2], want_r)
     y_def = (out[2].astype(np.float32) * wn.astype(np.float32)).astype(np.float16)
     np.testing.assert_array_equal(out[4].view(np.uint16), y_def.view(np.uint16))
     np.testing.assert_array_equal(out[5].view(np.uint32), _ss_ref(out[2]).view(np.uint32))
     return out[4], out[5], want_r, wn
+
+
+@pytest.mark.parametrize("m,ko,dm", [(32, 2048, 2048), (5, 192, 100)])
+def test_fused_prenorm_flags_f16_overflow(m, ko, dm):
+    # Y = f16(R Wn) overflows where |R Wn| >= 65520: one row's residual entry
+    # set to 3e4 with its norm weight 4 must set OVF[0] (the fused kernel at
+    # 32 x 2048, the fallback at 5 x 100); R stays exact against the oracle.
+    _say("fused prenorm overflow flag", m, ko, dm)
+    r = oracle.Rng(77 + m)
+    x = r.tensor("f16", [m, ko], 1.0)
+    w = r.tensor("f16", [dm, ko], 1.0 / np.sqrt(ko))
+    res = r.tensor("f32", [m, dm], 1.0)
+    res[m // 2, dm // 3] = 3e4
+    wn = r.tensor("f16", [dm], 1.0)
+    wn[dm // 3] = 4.0
+    nb = (dm + 7) // 8
+    out = T.run("fused", "linear_residual_prenorm",
+                [x, w, res.copy(), wn, np.zeros((m, dm), np.float16), np.zeros((nb, m), np.float32),
+                 np.zeros(1, np.int32)], outputs=[2, 4, 6])
+    parity("prenorm R", out[2], oracle.linear_residual(x, w, res.copy()))
+    assert np.isinf(out[4][m // 2, dm // 3])
+    assert out[6][0] == 1
 
 
 @pytest.mark.parametrize("m,ko,dm,f", [(32, 2048, 2048, 5632), (17, 5632, 2048, 5632), (9, 1024, 1024, 4000),
@@ -671,9 +695,10 @@ def test_fused_prenorm_then_qkv_rs_rope_kv(cfgname, t):
     # The engine's decode-step pair for the next layer's attention input: the
     # down projection leaves Y = f16(R Wn) and the sums of squares, and
     # qkv_rs_rope_kv scales each row's QKV sums by 1 / rms(R) before the
-    # f16 rounding, the rotation and the cache write: against qkv_rope_kv of
-    # the oracle's rmsnorm(R) (within the float tolerance; slots and positions
-    # outside the tables included). t = 40 and the tiny config take the
+    # f16 rounding, the rotation and the cache write: against the oracle's
+    # rmsnorm -> llm/linear -> rope_q / kv_write chain (within the float
+    # tolerance; slots and positions outside the tables included; cache slots
+    # nobody writes bit-exact). t = 40 and the tiny config take the
     # fallbacks.
     _say("fused prenorm + qkv_rs_rope_kv", cfgname, t)
     cfg = getattr(oracle.Config, cfgname)()
@@ -694,12 +719,24 @@ def test_fused_prenorm_then_qkv_rs_rope_kv(cfgname, t):
     got = T.run("fused", "qkv_rs_rope_kv",
                 [y, wq, z(t, W), pos, slot, c, s, z(t, H, D), Kc.copy(), Vc.copy(), z(t, G, D), z(t, G, D), ss],
                 [T.F32(cfg.eps)])
+    # The oracle's chain: rmsnorm of R, llm/linear, then llm/rope_q and
+    # llm/kv_write of that QKV (src/llm/engine.rs launch order).
     bc = 1 << (dm - 1).bit_length()
     h = oracle.rmsnorm(want_r.astype(np.float32), wn, cfg.eps, BC=bc)
-    want = T.run("fused", "qkv_rope_kv", [h, wq, z(t, W), pos, slot, c, s, z(t, H, D), Kc.copy(), Vc.copy(),
-                                          z(t, G, D), z(t, G, D)])
-    for i, name in ((7, "Q"), (8, "Kc"), (9, "Vc"), (10, "K"), (11, "V")):
-        parity(f"qkv_rs {name}", got[i], want[i])
+    qkv = oracle.llm_linear(h, wq)  # (the fused kernel leaves its QKV argument unwritten)
+    want_q = oracle.rope_q(qkv, pos, c, s, H, D)
+    wKc, wVc, wK, wV = oracle.kv_write(qkv, pos, slot, c, s, Kc.copy(), Vc.copy(), z(t, G, D), z(t, G, D))
+    for i, name, want in ((7, "Q", want_q), (8, "Kc", wKc), (9, "Vc", wVc), (10, "K", wK), (11, "V", wV)):
+        parity(f"qkv_rs {name}", got[i], want)
+    # Slots outside [0, NS) (the last two rows) write nothing: every cache
+    # slot no row wrote keeps its bits.
+    written = set(int(x) for x in slot if 0 <= x < NS)
+    untouched = [i for i in range(NS) if i not in written]
+    np.testing.assert_array_equal(got[8][untouched].view(np.uint16), Kc[untouched].view(np.uint16))
+    np.testing.assert_array_equal(got[9][untouched].view(np.uint16), Vc[untouched].view(np.uint16))
+    # A position past the rotary tables (row 0) rotates by zeros, as the
+    # oracle's rope_q does: its Q row is all zero on both sides.
+    assert not want_q[0].any() and not got[7][0].any()
 
 
 @pytest.mark.parametrize("cfgname", ["tiny", "tinyllama"])

@@ -91,3 +91,33 @@ def test_request_checks():
         T.schedule_trace(lim, 1, [([], 2)], 4, True, [[0, 0]])
     steps, toks, _ = T.schedule_trace(lim, 1, [([1, 2], 1)], 4, True, [[5]])
     assert toks == [[5]] and len(steps) == 1
+
+
+def test_schedule_trace_rejects_null_arguments():
+    # With requests present, a null prompts / offsets / max_new / script /
+    # output pointer is an argument error (TSL_ERR_ARG), not a host read
+    # out of bounds.
+    import ctypes
+
+    import numpy as np
+    L = T.lib()
+    lim = T.Limits(8, 16, 32, 4)
+    prompts = np.array([1, 2, 3], np.int32)
+    offsets = np.array([0, 3], np.int64)
+    max_new = np.array([2], np.int32)
+    script = np.array([5, 6], np.int32)
+    out = np.zeros(2, np.int32)
+    counts = np.zeros(1, np.int32)
+    trace = np.zeros(256, np.int32)
+    used = ctypes.c_int64(0)
+    full = [prompts.ctypes.data, offsets.ctypes.data, max_new.ctypes.data, script.ctypes.data, out.ctypes.data,
+            counts.ctypes.data]
+    for hole in range(len(full)):
+        p = list(full)
+        p[hole] = None
+        r = L.tsl_schedule_trace(ctypes.byref(lim), -1, 1, p[0], p[1], p[2], 2, 1, p[3], p[4], p[5], None,
+                                 trace.ctypes.data, 256, ctypes.byref(used))
+        assert r != 0 and b"null" in L.tsl_last_error(), hole
+    r = L.tsl_schedule_trace(ctypes.byref(lim), -1, 1, *full[:3], 2, 1, *full[3:], None, trace.ctypes.data, 256,
+                             ctypes.byref(used))
+    assert r == 0 and out.tolist() == [5, 6]
