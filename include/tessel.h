@@ -200,6 +200,13 @@ int tsl_engine_graphs(int engine, int32_t* rows, int32_t* graphs, int cap, int* 
  * with every norm applied first; *n gets how many steps were. */
 int tsl_engine_fallbacks(int engine, int64_t* n);
 
+/* No counterpart in the reference: decode-step timing. From this call on
+ * (on != 0), each decode step's GPU span (its input upload to the end of its
+ * last kernel, by events on the stream) is summed, apart for graph replays
+ * (index 0) and eager launches (index 1). The call returns, in steps[2] and
+ * ms[2], what was summed since the previous call, and clears it. */
+int tsl_engine_step_times(int engine, int on, int64_t* steps, double* ms);
+
 /* Engine::step (src/llm/engine.rs:275-354). mode 0 = Prefill, 1 = Packed
  * (starts[n]), 2 = Decode (tables: nseq rows of max_seq_pages pages, lens:
  * nseq). logits receives nwant * vocab floats for rows want[0..nwant). */

@@ -319,8 +319,9 @@ def forward(cfg, weights, tokens):
     embed, layers, norm, head = weights
     tokens = np.ascontiguousarray(tokens, np.int32)
     out = np.zeros((tokens.size, cfg.vocab), np.float32)
-    lib().tsl_ref_forward(ctypes.byref(cfg), _p(embed), _p(layers), _p(norm), _p(head), _p(tokens), tokens.size,
-                          _p(out))
+    if lib().tsl_ref_forward(ctypes.byref(cfg), _p(embed), _p(layers), _p(norm), _p(head), _p(tokens), tokens.size,
+                             _p(out)) != 0:
+        raise ValueError(f"forward: {tokens.size} tokens, more than max_pos = {cfg.max_pos}")
     return out
 
 

@@ -6,6 +6,7 @@
 // sequence at a time: the oracle the engine's logits are checked against).
 // f32 sums are sequential in f32, as Rust's Iterator::sum over f32 is.
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -95,43 +96,78 @@ i64 tsl_ref_argmax(const float* xs, i64 n) {
     return best;
 }
 
+// s[j] = sum over k, in k order, of w[k] * xt[k * 16 + j], for 16 tokens j
+// side by side (independent f32 chains: vector lanes, never reassociated).
+// Built for AVX2 as well as the baseline, picked at load time.
+__attribute__((target_clones("avx2", "default"))) static void dot_block(const float* w, const float* xt, i64 cols,
+                                                                        float* s) {
+    typedef float v8 __attribute__((vector_size(32)));
+    v8 a0 = {}, a1 = {};
+    for (i64 k = 0; k < cols; k++) {
+        v8 x0, x1;
+        std::memcpy(&x0, xt + k * 16, 32);
+        std::memcpy(&x1, xt + k * 16 + 8, 32);
+        const float wk = w[k];
+        a0 += wk * x0;  // a multiply, then an add (no contraction: -ffp-contract=off)
+        a1 += wk * x1;
+    }
+    std::memcpy(s, &a0, 32);
+    std::memcpy(s + 8, &a1, 32);
+}
+
 // reference::forward (src/llm/reference.rs:38-108): logits after each of
-// the n tokens, into out[n * vocab].
+// the n tokens, into out[n * vocab]. The reference runs token by token; this
+// runs layer by layer over all n tokens (position order inside each layer),
+// which performs every scalar operation of the token-by-token order in the
+// same sequence per token (attention at position p reads the keys of
+// positions <= p of the same layer, all present), so the bits are the same,
+// while each weight row is read once per layer for all n tokens.
 int tsl_ref_forward(const Cfg* cfg, const u16* embed, const u16* layers, const u16* norm, const u16* head,
                     const i32* tokens, i64 n, float* out) {
     const Cfg& c = *cfg;
     const i64 hd = c.head_dim, nh = c.heads, ng = c.kv_heads, dm = c.dim, ff = c.ffn;
-    auto f = [](const u16* v, i64 n) {
-        std::vector<float> r(n);
-        for (i64 i = 0; i < n; i++) r[i] = tsl_ref_f16_to_f32(v[i]);
-        return r;
-    };
-    auto matvec = [](const std::vector<float>& w, const std::vector<float>& x, i64 rows) {
-        i64 cols = (i64)x.size();
-        std::vector<float> y(rows);
-        // Rows in parallel; each row's sum stays the sequential f32 loop.
-#pragma omp parallel for schedule(static) if (rows * cols > (1 << 20))
-        for (i64 r = 0; r < rows; r++) {
-            float s = 0.0f;
-            for (i64 k = 0; k < cols; k++) s += w[r * cols + k] * x[k];
-            y[r] = s;
+    typedef std::vector<float> vf;
+    // y[t][r] = sum_k w[r][k] x[t][k], the sequential f32 loop per (t, r);
+    // rows in parallel, the f16 weight row converted once for all t.
+    auto matmul = [n](const u16* w, const std::vector<vf>& x, i64 rows, std::vector<vf>& y) {
+        const i64 cols = (i64)x[0].size();
+        y.assign(n, vf(rows));
+        constexpr int TB = 16;
+        const i64 nb = (n + TB - 1) / TB;
+        vf xT((size_t)nb * cols * TB, 0.0f);  // [token block][k][TB]
+        for (i64 t = 0; t < n; t++)
+            for (i64 k = 0; k < cols; k++) xT[((size_t)(t / TB) * cols + k) * TB + t % TB] = x[t][k];
+#pragma omp parallel
+        {
+            vf wr(cols);
+#pragma omp for schedule(static)
+            for (i64 r = 0; r < rows; r++) {
+                for (i64 k = 0; k < cols; k++) wr[k] = tsl_ref_f16_to_f32(w[r * cols + k]);
+                // TB tokens' sums side by side (independent chains, each in k order).
+                for (i64 t0 = 0; t0 < n; t0 += TB) {
+                    const i64 nt = std::min<i64>(TB, n - t0);
+                    const float* xt = &xT[(size_t)(t0 / TB) * cols * TB];
+                    float s[TB];
+                    dot_block(wr.data(), xt, cols, s);
+                    for (i64 j = 0; j < nt; j++) y[t0 + j][r] = s[j];
+                }
+            }
         }
-        return y;
     };
-    auto rmsnorm = [](const std::vector<float>& x, const std::vector<float>& w, float eps) {
+    auto rmsnorm = [](const vf& x, const u16* w16, float eps) {
         float ms = 0.0f;
         for (float v : x) ms += v * v;
         ms = ms / (float)x.size();
         float s = 1.0f / std::sqrt(ms + eps);
-        std::vector<float> y(x.size());
-        for (size_t i = 0; i < x.size(); i++) y[i] = x[i] * s * w[i];
+        vf y(x.size());
+        for (size_t i = 0; i < x.size(); i++) y[i] = x[i] * s * tsl_ref_f16_to_f32(w16[i]);
         return y;
     };
-    std::vector<float> cs((i64)c.max_pos * (hd / 2)), sn(cs.size());
+    vf cs((i64)c.max_pos * (hd / 2)), sn(cs.size());
     tsl_ref_rope_tables(cfg, cs.data(), sn.data());
-    auto rope = [&](std::vector<float>& x, i64 pos) {
+    auto rope = [&](float* x, i64 len, i64 pos) {
         i64 h = hd / 2;
-        for (size_t base = 0; base < x.size(); base += hd)
+        for (i64 base = 0; base < len; base += hd)
             for (i64 i = 0; i < h; i++) {
                 float cc = cs[pos * h + i], ss = sn[pos * h + i];
                 float a = x[base + i], b = x[base + i + h];
@@ -139,75 +175,66 @@ int tsl_ref_forward(const Cfg* cfg, const u16* embed, const u16* layers, const u
                 x[base + i + h] = b * cc + a * ss;
             }
     };
-    struct L {
-        std::vector<float> n1, wqkv, wo, n2, wg, wu, wd;
-    };
-    std::vector<L> ls;
-    const u16* p = layers;
-    i64 qr = (nh + 2 * ng) * hd;
-    for (int l = 0; l < c.layers; l++) {
-        L x;
-        x.n1 = f(p, dm);
-        p += dm;
-        x.wqkv = f(p, qr * dm);
-        p += qr * dm;
-        x.wo = f(p, dm * nh * hd);
-        p += dm * nh * hd;
-        x.n2 = f(p, dm);
-        p += dm;
-        x.wg = f(p, ff * dm);
-        p += ff * dm;
-        x.wu = f(p, ff * dm);
-        p += ff * dm;
-        x.wd = f(p, dm * ff);
-        p += dm * ff;
-        ls.push_back(std::move(x));
+    if (n <= 0) return 0;
+    if (n > c.max_pos) return -1;  // the reference's rope table index panics past max_pos
+    const i64 qr = (nh + 2 * ng) * hd;
+    std::vector<vf> x(n), h(n), y, y2;
+    for (i64 t = 0; t < n; t++) {
+        x[t].resize(dm);
+        for (i64 i = 0; i < dm; i++) x[t][i] = tsl_ref_f16_to_f32(embed[(i64)tokens[t] * dm + i]);
     }
-    std::vector<float> emb = f(embed, (i64)c.vocab * dm), nrm = f(norm, dm), hw = f(head, (i64)c.vocab * dm);
-    std::vector<std::vector<std::vector<float>>> kc(c.layers), vc(c.layers);
-    for (i64 pos = 0; pos < n; pos++) {
-        i64 t = tokens[pos];
-        std::vector<float> x(emb.begin() + t * dm, emb.begin() + (t + 1) * dm);
-        for (int li = 0; li < c.layers; li++) {
-            const L& w = ls[li];
-            std::vector<float> h = rmsnorm(x, w.n1, c.eps);
-            std::vector<float> qkv = matvec(w.wqkv, h, qr);
-            std::vector<float> q(qkv.begin(), qkv.begin() + nh * hd);
-            std::vector<float> k(qkv.begin() + nh * hd, qkv.begin() + (nh + ng) * hd);
-            std::vector<float> v(qkv.begin() + (nh + ng) * hd, qkv.end());
-            rope(q, pos);
-            rope(k, pos);
-            kc[li].push_back(k);
-            vc[li].push_back(v);
-            std::vector<float> o(nh * hd, 0.0f);
+    const u16* p = layers;
+    for (int li = 0; li < c.layers; li++) {
+        const u16 *n1 = p, *wqkv = n1 + dm, *wo = wqkv + qr * dm, *n2 = wo + dm * nh * hd, *wg = n2 + dm,
+                  *wu = wg + ff * dm, *wd = wu + ff * dm;
+        p = wd + dm * ff;
+        for (i64 t = 0; t < n; t++) h[t] = rmsnorm(x[t], n1, c.eps);
+        matmul(wqkv, h, qr, y);  // y[t] = qkv of token t
+        for (i64 t = 0; t < n; t++) {
+            rope(y[t].data(), nh * hd, t);                // q
+            rope(y[t].data() + nh * hd, ng * hd, t);      // k
+        }
+        std::vector<vf> o(n, vf(nh * hd, 0.0f));
+#pragma omp parallel for schedule(dynamic)
+        for (i64 t = 0; t < n; t++) {
+            const float* q = y[t].data();
             for (i64 hh = 0; hh < nh; hh++) {
                 i64 g = hh / (nh / ng);
-                std::vector<float> sc;
-                for (auto& kk : kc[li]) {
+                vf sc;
+                for (i64 j = 0; j <= t; j++) {
+                    const float* kk = y[j].data() + nh * hd;
                     float s = 0.0f;
                     for (i64 d = 0; d < hd; d++) s += kk[g * hd + d] * q[hh * hd + d];
                     sc.push_back(s / std::sqrt((float)hd));
                 }
                 float m = -INFINITY;
                 for (float s : sc) m = std::fmax(m, s);
-                std::vector<float> e;
+                vf e;
                 float z = 0.0f;
                 for (float s : sc) e.push_back(std::exp(s - m));
                 for (float v2 : e) z += v2;
-                for (size_t j = 0; j < e.size(); j++)
-                    for (i64 d = 0; d < hd; d++) o[hh * hd + d] += e[j] / z * vc[li][j][g * hd + d];
+                for (size_t j = 0; j < e.size(); j++) {
+                    const float* vv = y[j].data() + (nh + ng) * hd;
+                    for (i64 d = 0; d < hd; d++) o[t][hh * hd + d] += e[j] / z * vv[g * hd + d];
+                }
             }
-            std::vector<float> ao = matvec(w.wo, o, dm);
-            for (i64 i = 0; i < dm; i++) x[i] += ao[i];
-            h = rmsnorm(x, w.n2, c.eps);
-            std::vector<float> g = matvec(w.wg, h, ff), u = matvec(w.wu, h, ff), a(ff);
-            for (i64 i = 0; i < ff; i++) a[i] = g[i] / (1.0f + std::exp(-g[i])) * u[i];
-            std::vector<float> dn = matvec(w.wd, a, dm);
-            for (i64 i = 0; i < dm; i++) x[i] += dn[i];
         }
-        std::vector<float> lg = matvec(hw, rmsnorm(x, nrm, c.eps), c.vocab);
-        std::memcpy(out + pos * c.vocab, lg.data(), sizeof(float) * c.vocab);
+        matmul(wo, o, dm, y2);
+        for (i64 t = 0; t < n; t++) {
+            for (i64 i = 0; i < dm; i++) x[t][i] += y2[t][i];
+            h[t] = rmsnorm(x[t], n2, c.eps);
+        }
+        matmul(wg, h, ff, y);
+        matmul(wu, h, ff, y2);
+        for (i64 t = 0; t < n; t++)
+            for (i64 i = 0; i < ff; i++) y[t][i] = y[t][i] / (1.0f + std::exp(-y[t][i])) * y2[t][i];
+        matmul(wd, y, dm, y2);
+        for (i64 t = 0; t < n; t++)
+            for (i64 i = 0; i < dm; i++) x[t][i] += y2[t][i];
     }
+    for (i64 t = 0; t < n; t++) h[t] = rmsnorm(x[t], norm, c.eps);
+    matmul(head, h, c.vocab, y);
+    for (i64 t = 0; t < n; t++) std::memcpy(out + t * c.vocab, y[t].data(), sizeof(float) * c.vocab);
     return 0;
 }
 

@@ -51,7 +51,7 @@ EXPORTS = [
     "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
     "tsl_checkpoint_save", "tsl_json_roundtrip", "tsl_rng_new", "tsl_rng_bits", "tsl_rng_tensor",
     "tsl_time_each", "tsl_engine_profile", "tsl_engine_profile_rows", "tsl_schedule_trace",
-    "tsl_graph_nodes", "tsl_engine_graphs", "tsl_engine_fallbacks", "tsl_probe_mfma", "tsl_probe_stream",
+    "tsl_graph_nodes", "tsl_engine_graphs", "tsl_engine_fallbacks", "tsl_engine_step_times", "tsl_probe_mfma", "tsl_probe_stream",
     "tsl_decode_attention_noalloc",
 ]
 
@@ -122,6 +122,7 @@ def _declare(L):
     L.tsl_probe_stream.argtypes = [_U64, ctypes.c_size_t, ctypes.c_size_t, _INT, ctypes.POINTER(ctypes.c_double)]
     L.tsl_engine_graphs.argtypes = [_INT, _P, _P, _INT, ctypes.POINTER(_INT)]
     L.tsl_engine_fallbacks.argtypes = [_INT, ctypes.POINTER(_I64)]
+    L.tsl_engine_step_times.argtypes = [_INT, _INT, _P, _P]
     L.tsl_decode_attention_noalloc.argtypes = [_U64] * 6 + [ctypes.c_float] + [_INT] * 7
     L.tsl_schedule_trace.argtypes = [ctypes.POINTER(Limits), _INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, _P,
                                      ctypes.POINTER(Stats), _P, _I64, ctypes.POINTER(_I64)]
@@ -493,6 +494,14 @@ class Engine:
         n = _I64()
         check(lib().tsl_engine_fallbacks(self.handle, ctypes.byref(n)))
         return n.value
+
+    def step_times(self, on=True):
+        """Decode-step GPU spans summed since the previous call (then
+        cleared; timing on from now when `on`): {"graph": (steps, ms),
+        "eager": (steps, ms)}."""
+        n, ms = np.zeros(2, np.int64), np.zeros(2, np.float64)
+        check(lib().tsl_engine_step_times(self.handle, int(bool(on)), n.ctypes.data, ms.ctypes.data))
+        return {"graph": (int(n[0]), float(ms[0])), "eager": (int(n[1]), float(ms[1]))}
 
     def profile(self, on):
         """Gpu::profile: time every launch on its own (graphs off) from now."""

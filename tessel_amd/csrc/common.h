@@ -28,6 +28,7 @@ typedef uint16_t u16;
 // reference's emulator does with its shared memory). Off in normal builds.
 #ifdef TSL_POISON_LDS
 #define TSL_POISON(arr) tsl_poison_lds(&(arr), sizeof(arr))
+#define TSL_POISON_BYTES(ptr, bytes) tsl_poison_lds((ptr), (bytes))
 __device__ inline void tsl_poison_lds(void* p, unsigned bytes) {
     uint32_t* w = static_cast<uint32_t*>(p);
     const unsigned nt = blockDim.x * blockDim.y * blockDim.z;
@@ -37,6 +38,7 @@ __device__ inline void tsl_poison_lds(void* p, unsigned bytes) {
 }
 #else
 #define TSL_POISON(arr) ((void)0)
+#define TSL_POISON_BYTES(ptr, bytes) ((void)0)
 #endif
 
 // Reinterpreting one element of an ext_vector in place,

@@ -482,6 +482,7 @@ template <int D, int QPG>
 __global__ __launch_bounds__(256) void decode_merge(DecArgs a) {
     constexpr int ST = QPG * (2 + D);  // floats per chunk state
     extern __shared__ float sm[];      // [nact][QPG][2 + D]
+    TSL_POISON_BYTES(sm, (unsigned)(a.NCH * ST * sizeof(float)));  // the launch's dynamic LDS
     const int bg = blockIdx.x, b = bg / a.G, g = bg % a.G;
     const int n = a.lens[b];
     const int npages = n > 0 ? (n + a.P - 1) / a.P : 0;

@@ -23,6 +23,7 @@
 #include "../../include/tessel.h"
 
 int tsl_fail(int code, const std::string& msg);
+int rt_event_rerecord(int id);
 
 namespace {
 
@@ -138,6 +139,13 @@ struct Engine {
     // projection (after the deferred form overflowed f16).
     bool plain = false;
     int64_t prenorm_fallbacks = 0;
+    // Decode-step timing (tsl_engine_step_times): the GPU span of each
+    // decode step, from its input upload to the end of its last kernel, by
+    // a pair of events; [0] graph replays, [1] eager launches.
+    bool time_steps = false;
+    int ev0 = -1, ev1 = -1;
+    int64_t timed_steps[2] = {0, 0};
+    double timed_ms[2] = {0.0, 0.0};
     // One device arena for a step's inputs, filled by one upload: for a step
     // of t (padded) rows, tok, pos, slot, idx, starts, lens (t ints each),
     // then table (t max_seq_pages ints). layout(t) points the buffers there;
@@ -455,14 +463,25 @@ struct Engine {
                 h_len[b] = ln_in[b];
             }
         }
-        TRY(write(in, 0, hin.data(), nin * 4));
         bool prefill = mode != DECODE;
+        const bool timed = time_steps && !prefill && !profiling;
+        if (timed) {
+            if (ev0 < 0) {
+                TRY(tsl_event_record(&ev0));
+                TRY(tsl_event_record(&ev1));
+            } else {
+                TRY(rt_event_rerecord(ev0));
+            }
+        }
+        TRY(write(in, 0, hin.data(), nin * 4));
+        bool replayed = false;
         phase = prefill ? "prefill" : "decode";
         // Profiling times every launch on its own, so it runs without graphs.
         if (!prefill && graphs && !profiling && bw == t) {
             auto it = graph.find(t);
             if (it != graph.end()) {
                 TRY(tsl_replay(it->second));
+                replayed = true;
             } else {
                 TRY(launch_all(t, false, bw));
                 TRY(tsl_sync());
@@ -477,6 +496,7 @@ struct Engine {
         } else {
             TRY(launch_all(t, prefill, bw));
         }
+        if (timed) TRY(rt_event_rerecord(ev1));
         if (uses_prenorm(t, prefill)) {
             // The deferred norms leave Y = f16(R Wn), which overflows where
             // |R Wn| >= 65520 although the normalised rows need not: such a
@@ -500,12 +520,21 @@ struct Engine {
                 TRY(r);
             } else if (out_tok && nwant) {
                 std::copy(dl.begin() + 4, dl.end(), out_tok);
-                return 0;
+                return timed ? add_step_time(replayed) : 0;
             }
         }
-        if (nwant == 0) return 0;
-        if (out_tok) return tsl_download(out_tok, next.p, nwant * 4);
-        return tsl_download(out, logits.p, nwant * (size_t)cfg.vocab * 4);
+        if (nwant > 0) {
+            if (out_tok) TRY(tsl_download(out_tok, next.p, nwant * 4));
+            else TRY(tsl_download(out, logits.p, nwant * (size_t)cfg.vocab * 4));
+        }
+        return timed ? add_step_time(replayed) : 0;
+    }
+    int add_step_time(bool replayed) {
+        float ms = 0.0f;
+        TRY(tsl_event_elapsed(ev0, ev1, &ms));
+        timed_steps[replayed ? 0 : 1]++;
+        timed_ms[replayed ? 0 : 1] += ms;
+        return 0;
     }
     std::vector<int32_t> dl;
 };
@@ -672,6 +701,19 @@ int tsl_engine_fallbacks(int engine, int64_t* n) {
     Engine* e = get(engine);
     if (!e || !n) return tsl_fail(TSL_ERR_ARG, "no such engine, or a null count");
     *n = e->prenorm_fallbacks;
+    return 0;
+}
+
+int tsl_engine_step_times(int engine, int on, int64_t* steps, double* ms) {
+    Engine* e = get(engine);
+    if (!e || !steps || !ms) return tsl_fail(TSL_ERR_ARG, "no such engine, or a null output");
+    for (int i = 0; i < 2; i++) {
+        steps[i] = e->timed_steps[i];
+        ms[i] = e->timed_ms[i];
+        e->timed_steps[i] = 0;
+        e->timed_ms[i] = 0.0;
+    }
+    e->time_steps = on != 0;
     return 0;
 }
 

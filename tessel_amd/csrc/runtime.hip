@@ -616,3 +616,12 @@ int tsl_event_elapsed(int start, int end, float* ms) {
 }
 
 }  // extern "C"
+
+// Records event `id` (made by tsl_event_record) again, on the stream: the
+// engine's per-step timing reuses one pair of events. Library-internal.
+int rt_event_rerecord(int id) {
+    NEED_OPEN();
+    if (id < 0 || id >= (int)g.events.size()) return tsl_fail(TSL_ERR_ARG, "no such event");
+    CHECK(hipEventRecord(g.events[id], g.stream), "record");
+    return 0;
+}

@@ -104,7 +104,15 @@ def test_graph_replay_matches_eager(gpu):
     outs = []
     for graphs in (False, True):
         e = T.Engine(cfg, limits(pages=64), w, graphs=graphs)
+        e.step_times(True)
         outs.append(e.generate(reqs, 3)[0])
+        # Every decode step was timed, as a replay or as eager launches (the
+        # first step of each batch size is launched eagerly, then captured).
+        tm = e.step_times(False)
+        n = tm["graph"][0] + tm["eager"][0]
+        print(f"graphs={graphs}: step spans {tm}", flush=True)
+        assert n > 0 and all(ms > 0 for k, ms in tm.values() if k)
+        assert (tm["graph"][0] > 0) == graphs
         if graphs:
             # The recorded decode steps are kernel launches only (no memset
             # or copy nodes): each layer's QKV, attention (+ merge), o and
@@ -178,27 +186,35 @@ def _tinyllama_engine(seqs=32, prompt=512, new=128, graphs=True):
 
 def test_tinyllama_shape_against_the_reference(gpu):
     """Config 5's model (22 layers, 32/4 heads, D 64, FFN 5632, vocab 32000)
-    against reference::forward (src/llm/reference.rs): prefill logits of a
-    24-token prompt at three rows, then a batched greedy generation whose
-    every token is the reference's argmax or within 2e-2 of its scale
-    (tests/llm.rs:26-82)."""
-    cfg, w, e = _tinyllama_engine(seqs=2, prompt=32, new=8)
+    against reference::forward (src/llm/reference.rs) at real context
+    lengths: prefill logits of a 124-token prompt at three rows, then four
+    prompts of 109-188 tokens packed into one prefill step (multi-page
+    tables, 7-12 pages each) and 10 greedy steps at batch 4 whose positions
+    each cross a 16-token page boundary; every token is the reference's
+    argmax or within 2e-2 of its scale (tests/llm.rs:26-82)."""
+    lens = (124, 157, 188, 109)
+    new = 10
+    cfg, w, e = _tinyllama_engine(seqs=4, prompt=max(lens), new=new)
     ocfg = oracle.Config.tinyllama()
     rng = np.random.default_rng(3)
-    p1 = rng.integers(3, cfg.vocab, 24).tolist()
-    p2 = rng.integers(3, cfg.vocab, 17).tolist()
+    prompts = [rng.integers(3, cfg.vocab, n).tolist() for n in lens]
+    for n in lens:  # positions n .. n + new - 2 feed decode steps; each run crosses a page boundary
+        assert (n - 1) // 16 != (n + new - 2) // 16
+    p1 = prompts[0]
     n = len(p1)
-    got = e.step(p1, list(range(n)), list(range(n)), T.Engine.PREFILL, want=[0, 11, n - 1])
-    reqs = [(p1, 8), (p2, 6)]
-    outs, st = e.generate(reqs, 2)
+    rows = (0, 63, n - 1)
+    got = e.step(p1, list(range(n)), list(range(n)), T.Engine.PREFILL, want=list(rows))
+    reqs = [(p, new) for p in prompts]
+    outs, st = e.generate(reqs, 4)
     e.close()
-    assert st.largest_batch == 2 and [len(o) for o in outs] == [8, 6]
+    print(f"tinyllama: {st.prefill_steps} prefill step(s), {st.decode_steps} decode steps", flush=True)
+    assert st.prefill_steps == 1 and st.largest_batch == 4 and [len(o) for o in outs] == [new] * 4
     exact = total = 0
     for k, ((p, m), toks) in enumerate(zip(reqs, outs)):
         seq = list(p) + toks[:-1]
         ref = oracle.forward(ocfg, w, seq)  # logits after every position of the history
         if k == 0:
-            for row, r in zip(got, (0, 11, n - 1)):
+            for row, r in zip(got, rows):
                 err = rel(row, ref[r])
                 print(f"tinyllama prefill row {r}: logits within {err:.2e} of the reference", flush=True)
                 assert err < 2e-2

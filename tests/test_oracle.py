@@ -390,3 +390,19 @@ def test_reference_forward_against_f64():
     want = _np_forward(cfg, w, toks)
     rel = np.abs(got - want).max() / np.abs(want).max()
     assert rel < 1e-4, rel
+
+
+def test_reference_forward_is_causal_and_token_blocked_exactly():
+    """forward runs layer by layer over every token in 16-token blocks; the
+    logits after token i must not depend on later tokens or on the block a
+    token falls in: a prefix's logits equal, bit for bit, the same rows of
+    the longer run (37 tokens: three blocks, the last ragged). A history
+    longer than max_pos is an error, as the reference's table index is."""
+    cfg = oracle.Config.tiny()
+    w = oracle.weights_random(cfg, 5)
+    toks = [(i * 37 + 3) % cfg.vocab for i in range(37)]
+    full = oracle.forward(cfg, w, toks)
+    for k in (1, 15, 16, 17, 33):
+        np.testing.assert_array_equal(oracle.forward(cfg, w, toks[:k]).view(np.uint32), full[:k].view(np.uint32))
+    with pytest.raises(ValueError):
+        oracle.forward(cfg, w, [1] * (cfg.max_pos + 1))
