@@ -362,8 +362,8 @@ def llm_case(T, seqs=32, prompt=512, new=128, graphs=True):
     outs, st = e.generate(reqs, seqs)
     # Where a decode step's time goes (untimed runs of the same workload):
     # the GPU span of each step (input upload to last kernel end, by events)
-    # under graph replay and under eager launches, the wall time per step,
-    # and the sum of the step's kernel times (every launch timed alone).
+    # under graph replay and under eager launches, and the wall time per
+    # step (the difference: the scheduler's host work and the token download).
     split = {}
     if graphs:
         e.step_times(True)
@@ -373,15 +373,11 @@ def llm_case(T, seqs=32, prompt=512, new=128, graphs=True):
         _, se = e.generate(reqs, seqs)
         te = e.step_times(False)["eager"]
         e.set(True, True)
-        e.profile(True)
-        _, sp = e.generate(reqs, seqs)
-        ksum = sum(r[3] for r in e.profile_rows() if r[0] == "decode")
-        e.profile(False)
         us = lambda ms, n: round(1e3 * ms / n, 1) if n else None
         split = {"step_split_us": {
             "graph_gpu_span": us(tg[1], tg[0]), "graph_wall": us(1e3 * sg.decode_seconds, sg.decode_steps),
             "eager_gpu_span": us(te[1], te[0]), "eager_wall": us(1e3 * se.decode_seconds, se.decode_steps),
-            "kernel_sum": us(ksum, sp.decode_steps), "steps": sg.decode_steps}}
+            "steps": sg.decode_steps}}
     e.close()
     return {"case": "llm_decode", "model": "TinyLlama-1.1B shape (random fp16 weights)", **split,
             "sequences": seqs, "prompt": prompt, "new_tokens": new,

@@ -1302,7 +1302,10 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny_lds(const u16* __re
                 asm volatile("" : "+v"(yv));  // rounded to f32, then to f16 (no fused multiply-convert)
                 const u16 yh = f2h(yv);
                 np.y[(size_t)em * N + n] = yh;
-                if ((yh & 0x7c00) == 0x7c00) *np.ovf = 1;  // inf or NaN: the caller normalises first instead
+                // An infinite Y from a finite R (an R that is NaN already, as
+                // in the padding rows of a decode step, whose attention over
+                // no keys is 0/0, is not flagged): the caller normalises first.
+                if ((yh & 0x7fff) == 0x7c00) *np.ovf = 1;
             }
             sq[(et * 8 + ej) * 16 + (el & 15)] = nv * nv;
         }
@@ -1922,7 +1925,7 @@ __global__ __launch_bounds__(256) void prenorm_kernel(const float* __restrict__ 
         asm volatile("" : "+v"(yv));  // rounded to f32, then to f16 (as the fused kernel)
         const u16 yh = f2h(yv);
         Y[(size_t)m * N + n] = yh;
-        if ((yh & 0x7c00) == 0x7c00) *ovf = 1;
+        if ((yh & 0x7fff) == 0x7c00) *ovf = 1;  // infinite (not NaN), as the fused kernel
         float q = v * v;
         asm volatile("" : "+v"(q));  // the product rounded, not contracted into an fma (as in the fused kernel)
         a += q;
@@ -1940,8 +1943,9 @@ int launch_qkv_rope_kv(TslKernel& k, const uint64_t* a, hipStream_t s) {
 // Y = f16(R Wn) and SS[b][m], the sum over the 8 columns n = 8 b .. 8 b + 7
 // (column order) of the new R[m][n]^2. Arguments X [M, K], W [N, K], R [M, N],
 // Wn [N], Y [M, N], SS [NB, M], NB = ceil(N / 8), OVF [1]. Y overflows f16
-// where |R Wn| >= 65520 although rmsnorm(R) Wn may not: then the kernel sets
-// OVF[0] = 1 (it never clears it) and the caller should normalise first
+// where |R Wn| >= 65520 although rmsnorm(R) Wn may not: then (Y infinite)
+// the kernel sets OVF[0] = 1 (it never clears it) and the caller should
+// normalise first
 // (fused/linear_residual_rmsnorm), as the engine does.
 int launch_linear_residual_prenorm(TslKernel& k, const uint64_t* a, hipStream_t s) {
     const int M = k.dim("M"), N = k.dim("N"), K = k.dim("K"), NB = k.dim("NB");
