@@ -75,7 +75,15 @@ TSL_DEV int swz_v(int key) {  // in 16-byte chunks
 // through LDS at the end (max, then the rescaled sums, in wavefront order).
 // D = 128 with the key split holds 4 stages of 32 KB: one workgroup per CU,
 // so its launch bounds ask for one (and the registers that allows).
-template <int D, bool PREFILL, int KS>
+//
+// FOLD: Q is scaled by c2 = scale log2(e) on its way into registers (rounded
+// to f16) and the score MFMAs start from -mc (a 16-register tile of this
+// lane's running max) instead of 0, so the accumulators are the exponents
+// and the per-score multiply-add goes. The tile costs registers: ~150
+// instead of 128, 3 workgroups per CU instead of 4, so it serves grids of at
+// most 3 workgroups per CU (S = 2048 at 32 heads: 517 -> 553 TFLOP/s, same
+// box); at S = 4096 (4 per CU) the unfolded form is faster (768 against 743).
+template <int D, bool PREFILL, int KS, bool FOLD>
 __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(AttnArgs a) {
     constexpr int DP = D < 32 ? 32 : D;     // V^T rows, padded to one MFMA tile
     constexpr int KCH = D / 8;              // 16-byte chunks per row
@@ -115,16 +123,20 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
     const char* Vh = reinterpret_cast<const char*>(a.V + (long)hk * a.k_head);
     const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
 
-    // Q^T operand, kept in registers: lane l holds d = 16 s + 8 (l/32) .. +8 of its query.
+    // Q^T operand, kept in registers: lane l holds d = 16 s + 8 (l/32) .. +8
+    // of its query (FOLD: times c2, rounded to f16).
+    const float c2 = a.scale * LOG2E;
     half8 qop[D / 16];
 #pragma unroll
     for (int s = 0; s < D / 16; s++) {
         u32x4 t = {0, 0, 0, 0};
         if (myq < a.S) t = *reinterpret_cast<const u32x4*>(Qh + (long)myq * a.q_row + 16 * s + 8 * g4);
         qop[s] = __builtin_bit_cast(half8, t);
+        if constexpr (FOLD)
+#pragma unroll
+            for (int e = 0; e < 8; e++) qop[s][e] = (half_t)((float)qop[s][e] * c2);
     }
     const int my_start = PREFILL ? (myq < a.S ? a.starts[myq] : 0) : 0;
-    const float c2 = a.scale * LOG2E;
 
     // This lane's byte offsets (relative to the block's first key row) for the
     // wave's K and V loads; the buffer base advances with the block.
@@ -187,6 +199,10 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
 
     float m = PREFILL ? -1e30f : -INFINITY;  // running max of raw scores
     float mc = PREFILL ? -1e30f * c2 : -INFINITY;  // the same, times c2
+    // FOLD: p = exp2(c2 s - mc) with mc the running max of the scaled scores
+    // (0 until a block sets it), and the score MFMAs start from nm = -mc.
+    if constexpr (FOLD) mc = 0.0f;
+    float16v nm = float16v{};
     float lsum = 0.0f;
     bool have_m = false;  // a block's max has set m
     float16v acc[DP / 32];
@@ -215,7 +231,7 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
 #pragma unroll
             for (int s = 0; s < D / 16; s++) {
                 const half8 kop = *reinterpret_cast<const half8*>(st_base + kaddr[kt][s]);
-                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[s], st[kt], 0, 0, 0);
+                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[s], FOLD && s == 0 ? nm : st[kt], 0, 0, 0);
             }
         }
         // Keys masked off: above the diagonal, past S and (prefill) before the
@@ -241,8 +257,10 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
 #pragma unroll
             for (int t = 0; t < 4; t++) {
 #pragma unroll
-                for (int hh = 0; hh < 8; hh++)
-                    pk[t][hh] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(st[t >> 1][8 * (t & 1) + hh], c2, -mc));
+                for (int hh = 0; hh < 8; hh++) {
+                    const float x = st[t >> 1][8 * (t & 1) + hh];
+                    pk[t][hh] = (half_t)__builtin_amdgcn_exp2f(FOLD ? x : __builtin_fmaf(x, c2, -mc));
+                }
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     lsum = __builtin_amdgcn_fdot2(half2v{pk[t][2 * e], pk[t][2 * e + 1]}, ones, lsum, false);
@@ -271,6 +289,29 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
             mb = fmaxf(mb, xor32(mb));
             // Lazy rescaling: the running max moves only when it would grow
             // by more than 2^LAZY.
+            if constexpr (FOLD) {
+                // mb is the block's largest exponent relative to mc (-inf where
+                // every key of the row is masked); the first block sets mc
+                // where it has a key.
+                const bool grow = have_m ? mb > LAZY : mb > -INFINITY;
+                if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+                    const float dm = have_m ? fmaxf(mb, 0.0f) : (mb > -INFINITY ? mb : 0.0f);
+                    if (have_m) {
+                        const float alpha = __builtin_amdgcn_exp2f(-dm);
+                        lsum *= alpha;
+#pragma unroll
+                        for (int dt = 0; dt < DP / 32; dt++) acc[dt] *= alpha;
+                    }
+#pragma unroll
+                    for (int kt = 0; kt < 2; kt++) st[kt] -= dm;
+                    mc += dm;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) nm[r] = -mc;
+                }
+                have_m = true;
+                exps();
+                goto block_done;
+            }
             const bool grow = mb * c2 > mc + LAZY;
             if (__builtin_amdgcn_ballot_w64(grow) != 0) {
                 const float mn = fmaxf(m, mb);
@@ -287,6 +328,7 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
             have_m = true;
             exps();
         }
+    block_done:
 #pragma unroll
         for (int dt = 0; dt < DP / 32; dt++) {
 #pragma unroll
@@ -313,7 +355,7 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
         __syncthreads();
         {
             float* me = st + wave * NF * 64 + lane;
-            me[0] = mc;
+            me[0] = FOLD && !have_m ? -INFINITY : mc;  // (FOLD: no block, no weight in the merge)
             me[64] = lsum;
 #pragma unroll
             for (int dt = 0; dt < DP / 32; dt++)
@@ -358,14 +400,14 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
 }
 
 
-template <bool PREFILL, int KS>
+template <bool PREFILL, int KS, bool FOLD>
 int run_attn_ks(AttnArgs a, int D, hipStream_t s, const char* what) {
     dim3 grid(((a.S + BQ / KS - 1) / (BQ / KS)) * a.H);
     switch (D) {
-        case 16: hipLaunchKernelGGL((attn_fwd<16, PREFILL, KS>), grid, dim3(256), 0, s, a); break;
-        case 32: hipLaunchKernelGGL((attn_fwd<32, PREFILL, KS>), grid, dim3(256), 0, s, a); break;
-        case 64: hipLaunchKernelGGL((attn_fwd<64, PREFILL, KS>), grid, dim3(256), 0, s, a); break;
-        case 128: hipLaunchKernelGGL((attn_fwd<128, PREFILL, KS>), grid, dim3(256), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((attn_fwd<16, PREFILL, KS, FOLD>), grid, dim3(256), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((attn_fwd<32, PREFILL, KS, FOLD>), grid, dim3(256), 0, s, a); break;
+        case 64: hipLaunchKernelGGL((attn_fwd<64, PREFILL, KS, FOLD>), grid, dim3(256), 0, s, a); break;
+        case 128: hipLaunchKernelGGL((attn_fwd<128, PREFILL, KS, FOLD>), grid, dim3(256), 0, s, a); break;
         default: return tsl_fail(-2, std::string(what) + ": head dimension " + std::to_string(D) +
                                          " unsupported (16, 32, 64 or 128)");
     }
@@ -382,8 +424,10 @@ int run_attn(AttnArgs a, int D, hipStream_t s, const char* what) {
     // split's halved K/V reuse costs more than the shorter critical path
     // gains (S=4096: 659 against 779), and a split of 4 (its stages fill the
     // LDS, one workgroup per CU) loses everywhere.
-    if ((long)((a.S + BQ - 1) / BQ) * a.H <= a.ncu) return run_attn_ks<PREFILL, 2>(a, D, s, what);
-    return run_attn_ks<PREFILL, 1>(a, D, s, what);
+    const long wgs = (long)((a.S + BQ - 1) / BQ) * a.H;
+    if (wgs <= a.ncu) return run_attn_ks<PREFILL, 2, false>(a, D, s, what);
+    if (wgs <= 3L * a.ncu) return run_attn_ks<PREFILL, 1, true>(a, D, s, what);  // (FOLD: see attn_fwd)
+    return run_attn_ks<PREFILL, 1, false>(a, D, s, what);
 }
 
 }  // namespace

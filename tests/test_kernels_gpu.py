@@ -244,23 +244,24 @@ def test_flash_attention_baseline_shapes(s):
 
 
 @pytest.mark.parametrize("name", ["flash_attention", "prefill_attention"])
-@pytest.mark.parametrize("s", [300, 2000])
-def test_attention_scores_that_outgrow_the_running_max(name, s):
+@pytest.mark.parametrize("s,h", [(300, 4), (2000, 4), (2000, 24)])
+def test_attention_scores_that_outgrow_the_running_max(name, s, h):
     # Keys of later blocks scaled up 12x (scores jump by far more than 2^16
     # in the exp2 domain): p against the stale running max overflows f16, and
     # the block is redone through its max. Short and long sequences (both
-    # key-split forms), plain and prefill (GQA, two packed prompts).
-    _say("attention growth", name, s)
+    # key-split forms, and at 24 heads the form with the scale folded into Q),
+    # plain and prefill (GQA, two packed prompts).
+    _say("attention growth", name, s, h)
     rng = np.random.default_rng(s + 7)
     if name == "flash_attention":
-        q, k, v = (rng.standard_normal((4, s, 64)).astype(np.float16) for _ in range(3))
+        q, k, v = (rng.standard_normal((h, s, 64)).astype(np.float16) for _ in range(3))
         k[:, s // 3:s // 3 + 40] *= np.float16(12)
         k[:, 2 * s // 3:] *= np.float16(3)
         want = oracle.flash_attention(q, k, v, 0.125, threads=8)
         got = T.run("attention", name, [q, k, v, np.zeros_like(q)], [T.F32(0.125)], outputs=[3])[3]
     else:
-        q = rng.standard_normal((s, 8, 64)).astype(np.float16)
-        k, v = (rng.standard_normal((s, 2, 64)).astype(np.float16) for _ in range(2))
+        q = rng.standard_normal((s, 2 * h, 64)).astype(np.float16)
+        k, v = (rng.standard_normal((s, h // 2, 64)).astype(np.float16) for _ in range(2))
         k[s // 3:s // 3 + 40] *= np.float16(12)
         starts = np.where(np.arange(s) < s // 2, 0, s // 2).astype(np.int32)
         want = oracle.prefill_attention(q, k, v, starts, 0.125, threads=8)
@@ -311,7 +312,8 @@ def _packed(seed, lens, h, g, d):
 
 
 @pytest.mark.parametrize("lens,h,g,d", [([90], 4, 2, 16), ([70, 20], 4, 2, 16), ([512, 512], 32, 4, 64),
-                                         ([300, 5, 130, 64], 8, 2, 64), ([1000], 32, 4, 64)])
+                                         ([300, 5, 130, 64], 8, 2, 64), ([1000], 32, 4, 64),
+                                         ([600, 7, 700, 300], 32, 4, 64), ([1500, 40], 32, 8, 128)])
 def test_prefill_attention_vs_oracle(lens, h, g, d):
     _say("prefill", lens, h, g, d)
     q, k, v, starts = _packed(11 + len(lens), lens, h, g, d)
