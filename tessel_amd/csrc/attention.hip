@@ -76,13 +76,16 @@ TSL_DEV int swz_v(int key) {  // in 16-byte chunks
 // D = 128 with the key split holds 4 stages of 32 KB: one workgroup per CU,
 // so its launch bounds ask for one (and the registers that allows).
 //
-// FOLD: Q is scaled by c2 = scale log2(e) on its way into registers (rounded
-// to f16) and the score MFMAs start from -mc (a 16-register tile of this
-// lane's running max) instead of 0, so the accumulators are the exponents
-// and the per-score multiply-add goes. The tile costs registers: ~150
-// instead of 128, 3 workgroups per CU instead of 4, so it serves grids of at
-// most 3 workgroups per CU (S = 2048 at 32 heads: 517 -> 553 TFLOP/s, same
-// box); at S = 4096 (4 per CU) the unfolded form is faster (768 against 743).
+// FOLD (KS = 1): Q is scaled by c2 = scale log2(e) on its way into
+// registers (rounded to f16) and the score MFMAs start from -mc (a
+// 16-register tile of this lane's running max) instead of 0, so the
+// accumulators are the exponents and the per-score multiply-add goes. A
+// block's two 32-key tiles are then computed and exponentiated one after the
+// other (the second tile's MFMAs can run under the first's exponentials), so
+// only one tile of scores is live and the -mc tile fits the 128 registers
+// that keep 4 workgroups per CU. Same box, H32 D64: S = 2048 502 -> 546,
+// S = 4096 781 -> 841 TFLOP/s. With the key split (KS = 2) the fold lost
+// (packed prefill 214 -> 170, S = 512 142 -> 137): that form stays unfolded.
 template <int D, bool PREFILL, int KS, bool FOLD>
 __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(AttnArgs a) {
     constexpr int DP = D < 32 ? 32 : D;     // V^T rows, padded to one MFMA tile
@@ -221,8 +224,110 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
         __syncthreads();                     // everyone's; and the last iteration's reads of the other stage are done
         if (it + 1 < nit) issue(it + 1, (it + 1) & 1, kbeg, nblk);
         const char* st_base = lds + (ks * 2 + (it & 1)) * STAGE;
+        // O^T += V^T P^T over the block's 4 k-steps.
+        auto pv = [&](const half8 (&pk)[4]) {
+#pragma unroll
+            for (int dt = 0; dt < DP / 32; dt++) {
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    half8 vop;
+                    if (D < 32 && (grp & 1)) {
+                        vop = half8{};  // V^T rows D .. 31 of the padded tile
+                    } else {
+                        const char* pvp = st_base + vaddr[dt] + 16 * t * ROWB;
+                        const half4 lo = lds_read_tr(pvp), hi = lds_read_tr(pvp + 8 * ROWB);
+                        vop = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                    }
+                    acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pk[t], acc[dt], 0, 0, 0);
+                }
+            }
+        };
         const bool active = b < nblk && j <= qw + 31 && qw < a.S;  // some key of this block <= some query of the wave
         if (!active) continue;
+        // Keys masked off: above the diagonal, past S and (prefill) before the
+        // row's own start. Key = j + 4 g + off_r with off_r a constant of the
+        // register, so each test is one compare against a per-lane limit.
+        const bool edge = PREFILL || j + BKEY - 1 > qw || j + BKEY > a.S;
+        const int hi_lim = min(myq, a.S - 1) - j - 4 * g4;                 // keep off_r <= hi_lim
+        const int lo_lim = PREFILL ? my_start - j - 4 * g4 : -(1 << 30);  // keep off_r >= lo_lim
+        auto mask = [&](float16v& t, int kt) {
+            if (!edge) return;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int off = kt * 32 + 8 * (r >> 2) + (r & 3);
+                bool keep = off <= hi_lim;
+                if (PREFILL) keep = keep && off >= lo_lim;
+                t[r] = keep ? t[r] : -INFINITY;
+            }
+        };
+        if constexpr (FOLD) {
+            // One 32-key tile at a time: S^T - mc (its MFMAs start from nm),
+            // masked, exponentiated; the second tile's MFMAs can run under
+            // the first's exponentials, and only one tile of scores is live.
+            auto tile = [&](int kt) {
+                float16v t = nm;
+#pragma unroll
+                for (int s2 = 0; s2 < D / 16; s2++) {
+                    const half8 kop = *reinterpret_cast<const half8*>(st_base + kaddr[kt][s2]);
+                    t = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[s2], t, 0, 0, 0);
+                }
+                mask(t, kt);
+                return t;
+            };
+            half8 pk[4];
+            auto exps2 = [&](const float16v& t, int kt) {
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int tt = 2 * kt + u;
+#pragma unroll
+                    for (int hh = 0; hh < 8; hh++) pk[tt][hh] = (half_t)__builtin_amdgcn_exp2f(t[8 * u + hh]);
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        lsum = __builtin_amdgcn_fdot2(half2v{pk[tt][2 * e], pk[tt][2 * e + 1]}, ones, lsum, false);
+                }
+            };
+            bool redo = !have_m;
+            if (have_m) {
+                const float l0 = lsum;
+                exps2(tile(0), 0);
+                exps2(tile(1), 1);
+                if (__builtin_amdgcn_ballot_w64(__builtin_isinf(lsum)) != 0) {
+                    lsum = l0;
+                    redo = true;
+                }
+            }
+            if (redo) {
+                // Both tiles again, the block's largest exponent relative to
+                // mc (-inf where every key of the row is masked); lazy
+                // rescaling: mc moves only when it would grow by more than
+                // 2^LAZY (the first block sets it where it has a key).
+                float16v t0 = tile(0), t1 = tile(1);
+                float mb = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 16; r++) mb = fmaxf(mb, fmaxf(t0[r], t1[r]));
+                mb = fmaxf(mb, xor32(mb));
+                const bool grow = have_m ? mb > LAZY : mb > -INFINITY;
+                if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+                    const float dm = have_m ? fmaxf(mb, 0.0f) : (mb > -INFINITY ? mb : 0.0f);
+                    if (have_m) {
+                        const float alpha = __builtin_amdgcn_exp2f(-dm);
+                        lsum *= alpha;
+#pragma unroll
+                        for (int dt = 0; dt < DP / 32; dt++) acc[dt] *= alpha;
+                    }
+                    t0 -= dm;
+                    t1 -= dm;
+                    mc += dm;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) nm[r] = -mc;
+                }
+                have_m = true;
+                exps2(t0, 0);
+                exps2(t1, 1);
+            }
+            pv(pk);
+            continue;
+        }
         // S^T = K Q^T for the 64 keys x this wave's 32 queries (two 32-key tiles).
         float16v st[2];
 #pragma unroll
@@ -231,25 +336,11 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
 #pragma unroll
             for (int s = 0; s < D / 16; s++) {
                 const half8 kop = *reinterpret_cast<const half8*>(st_base + kaddr[kt][s]);
-                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[s], FOLD && s == 0 ? nm : st[kt], 0, 0, 0);
+                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop[s], st[kt], 0, 0, 0);
             }
         }
-        // Keys masked off: above the diagonal, past S and (prefill) before the
-        // row's own start. Key = j + 4 g + off_r with off_r a constant of the
-        // register, so each test is one compare against a per-lane limit.
-        if (PREFILL || j + BKEY - 1 > qw || j + BKEY > a.S) {
-            const int hi_lim = min(myq, a.S - 1) - j - 4 * g4;  // keep off_r <= hi_lim
-            const int lo_lim = PREFILL ? my_start - j - 4 * g4 : -(1 << 30);  // keep off_r >= lo_lim
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int off = kt * 32 + 8 * (r >> 2) + (r & 3);
-                    bool keep = off <= hi_lim;
-                    if (PREFILL) keep = keep && off >= lo_lim;
-                    st[kt][r] = keep ? st[kt][r] : -INFINITY;
-                }
-        }
+        for (int kt = 0; kt < 2; kt++) mask(st[kt], kt);
         // P = exp2(s c2 - m c2), rounded to f16 as the .tl's f16(p); row sums
         // from the f16 pairs. Then O^T += V^T P^T over the block's 4 k-steps.
         half8 pk[4];
@@ -257,10 +348,8 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
 #pragma unroll
             for (int t = 0; t < 4; t++) {
 #pragma unroll
-                for (int hh = 0; hh < 8; hh++) {
-                    const float x = st[t >> 1][8 * (t & 1) + hh];
-                    pk[t][hh] = (half_t)__builtin_amdgcn_exp2f(FOLD ? x : __builtin_fmaf(x, c2, -mc));
-                }
+                for (int hh = 0; hh < 8; hh++)
+                    pk[t][hh] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(st[t >> 1][8 * (t & 1) + hh], c2, -mc));
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     lsum = __builtin_amdgcn_fdot2(half2v{pk[t][2 * e], pk[t][2 * e + 1]}, ones, lsum, false);
@@ -289,29 +378,6 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
             mb = fmaxf(mb, xor32(mb));
             // Lazy rescaling: the running max moves only when it would grow
             // by more than 2^LAZY.
-            if constexpr (FOLD) {
-                // mb is the block's largest exponent relative to mc (-inf where
-                // every key of the row is masked); the first block sets mc
-                // where it has a key.
-                const bool grow = have_m ? mb > LAZY : mb > -INFINITY;
-                if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-                    const float dm = have_m ? fmaxf(mb, 0.0f) : (mb > -INFINITY ? mb : 0.0f);
-                    if (have_m) {
-                        const float alpha = __builtin_amdgcn_exp2f(-dm);
-                        lsum *= alpha;
-#pragma unroll
-                        for (int dt = 0; dt < DP / 32; dt++) acc[dt] *= alpha;
-                    }
-#pragma unroll
-                    for (int kt = 0; kt < 2; kt++) st[kt] -= dm;
-                    mc += dm;
-#pragma unroll
-                    for (int r = 0; r < 16; r++) nm[r] = -mc;
-                }
-                have_m = true;
-                exps();
-                goto block_done;
-            }
             const bool grow = mb * c2 > mc + LAZY;
             if (__builtin_amdgcn_ballot_w64(grow) != 0) {
                 const float mn = fmaxf(m, mb);
@@ -328,22 +394,7 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
             have_m = true;
             exps();
         }
-    block_done:
-#pragma unroll
-        for (int dt = 0; dt < DP / 32; dt++) {
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                half8 vop;
-                if (D < 32 && (grp & 1)) {
-                    vop = half8{};  // V^T rows D .. 31 of the padded tile
-                } else {
-                    const char* pv = st_base + vaddr[dt] + 16 * t * ROWB;
-                    const half4 lo = lds_read_tr(pv), hi = lds_read_tr(pv + 8 * ROWB);
-                    vop = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                }
-                acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pk[t], acc[dt], 0, 0, 0);
-            }
-        }
+        pv(pk);
     }
 
     if constexpr (KS > 1) {
@@ -426,8 +477,7 @@ int run_attn(AttnArgs a, int D, hipStream_t s, const char* what) {
     // LDS, one workgroup per CU) loses everywhere.
     const long wgs = (long)((a.S + BQ - 1) / BQ) * a.H;
     if (wgs <= a.ncu) return run_attn_ks<PREFILL, 2, false>(a, D, s, what);
-    if (wgs <= 3L * a.ncu) return run_attn_ks<PREFILL, 1, true>(a, D, s, what);  // (FOLD: see attn_fwd)
-    return run_attn_ks<PREFILL, 1, false>(a, D, s, what);
+    return run_attn_ks<PREFILL, 1, true>(a, D, s, what);
 }
 
 }  // namespace
