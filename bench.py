@@ -176,6 +176,44 @@ def cpu_baseline(a, b, budget_s):
             "others": others}
 
 
+def vendor_gemm(T, sizes=(1024, 2048, 4096, 8192)):
+    """hipBLASLt through torch (torch.matmul: A B with B [K, N], the matmul.tl
+    layout; F.linear: A B^T with B^T [N, K]) against this library's matmul,
+    in the same process, on N(0,1)/sqrt(K) f16 inputs: back-to-back launches
+    timed with torch's events (torch's stream) and with the library's."""
+    import torch
+
+    def timed(f, n):
+        for _ in range(20):
+            f()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            f()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    out = []
+    for n in sizes:
+        g = torch.Generator(device="cuda").manual_seed(n)
+        a = (torch.randn(n, n, device="cuda", generator=g) / n ** 0.5).half()
+        b = (torch.randn(n, n, device="cuda", generator=g) / n ** 0.5).half()
+        bt = b.t().contiguous()
+        fl = 2.0 * n ** 3
+        iters = 200 if n < 8192 else 40
+        nn = timed(lambda: torch.matmul(a, b), iters)
+        nt = timed(lambda: torch.nn.functional.linear(a, bt), iters)
+        t, _, _ = gemm_case(T, n, seed=n)
+        t.warm()
+        ours = t.median(iters)
+        out.append({"case": f"vendor gemm {n}^3", "hipblaslt_nn_tflops": round(fl / nn / 1e9, 1),
+                    "hipblaslt_nt_tflops": round(fl / nt / 1e9, 1), "ours_nn_tflops": round(fl / ours / 1e9, 1)})
+        del a, b, bt
+    return out
+
+
 def attention_case(T, s, seed=1):
     rng = np.random.default_rng(seed)
     h, d = 32, 64
@@ -402,7 +440,8 @@ def main():
                     help="TinyLlama case: launch decode steps kernel by kernel (for kernel traces)")
     ap.add_argument("--only", default="", help="comma list of cases: gemm1024,gemm2048,fa512..fa4096,decode,paged,"
                     "prefill,proj,probes,"
-                    "rmsnorm,softmax,llm,copy (counter calibration); 'none' for the headline GEMM alone")
+                    "rmsnorm,softmax,llm,copy (counter calibration),vendor (hipBLASLt via torch, opt-in); "
+                    "'none' for the headline GEMM alone")
     ap.add_argument("--profile", action="store_true",
                     help="few launches, no clock warm-up: for rocprofv3 counter passes")
     args = ap.parse_args()
@@ -511,6 +550,8 @@ def main():
             m = t.median(20)
             cases.append({"case": "add f32 32Mi (reads 256 MiB, writes 128 MiB)", "ms": round(m, 5),
                           "gbps": round(12.0 * n / m / 1e6, 1)})
+        if "vendor" in only:  # the vendor library on the same inputs (opt-in: torch / hipBLASLt), not a bench line
+            cases += vendor_gemm(T)
         if want("probes"):
             # Calibration, not bench lines: what the matrix cores sustain on the
             # GEMM's MFMA pattern with random against nearly constant operands
