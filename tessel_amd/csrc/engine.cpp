@@ -24,6 +24,10 @@
 
 int tsl_fail(int code, const std::string& msg);
 int rt_event_rerecord(int id);
+int rt_host_alloc(size_t n, void** p);
+int rt_host_free(void* p);
+int rt_upload_async(uint64_t dst, const void* pinned, size_t n);
+int rt_download_pinned(void* pinned, uint64_t src, size_t n);
 
 namespace {
 
@@ -151,7 +155,11 @@ struct Engine {
     // then table (t max_seq_pages ints). layout(t) points the buffers there;
     // the addresses depend only on t, so a graph captured for t stays valid.
     Buf in;
-    std::vector<int32_t> hin;
+    // Pinned host staging: a step's inputs (enqueued without a wait: the
+    // step's download synchronises before the next step rewrites them) and
+    // its flag and token ids (one enqueued copy, one wait).
+    int32_t* hin = nullptr;
+    int32_t* hout = nullptr;
     void layout(size_t t) {
         const size_t mp = lim.max_seq_pages;
         Buf* parts[] = {&tok, &pos, &slot, &idx, &starts, &lens};
@@ -302,6 +310,8 @@ struct Engine {
         TRY(alloc(t * d * 2, last));
         TRY(alloc(t * (size_t)cfg.vocab * 4, logits));
         TRY(alloc(t * (6 + (size_t)lim.max_seq_pages) * 4, in));
+        TRY(rt_host_alloc(t * (6 + (size_t)lim.max_seq_pages) * 4, reinterpret_cast<void**>(&hin)));
+        TRY(rt_host_alloc(16 + t * 4, reinterpret_cast<void**>(&hout)));
         TRY(alloc(16 + t * 4, outw));
         ovf = Buf{outw.p, 4};
         next = Buf{outw.p + 16, t * 4};
@@ -445,7 +455,7 @@ struct Engine {
         // Every input of the step in the arena's layout for t, one upload.
         layout(t);
         const size_t nin = 6 * t + (mode == DECODE ? t * mp : 0);
-        hin.assign(nin, 0);
+        std::memset(hin, 0, nin * 4);
         int32_t *h_tok = &hin[0], *h_pos = &hin[t], *h_slot = &hin[2 * t], *h_idx = &hin[3 * t];
         int32_t *h_st = &hin[4 * t], *h_len = &hin[5 * t];
         std::copy(tokens, tokens + n, h_tok);
@@ -473,7 +483,7 @@ struct Engine {
                 TRY(rt_event_rerecord(ev0));
             }
         }
-        TRY(write(in, 0, hin.data(), nin * 4));
+        TRY(rt_upload_async(in.p, hin, nin * 4));
         bool replayed = false;
         phase = prefill ? "prefill" : "decode";
         // Profiling times every launch on its own, so it runs without graphs.
@@ -504,9 +514,8 @@ struct Engine {
             // steps do (the step's KV writes are the same slots, rewritten).
             int32_t flag = 0;
             if (out_tok && nwant) {
-                dl.resize(4 + nwant);
-                TRY(tsl_download(dl.data(), outw.p, 16 + nwant * 4));
-                flag = dl[0];
+                TRY(rt_download_pinned(hout, outw.p, 16 + nwant * 4));
+                flag = hout[0];
             } else {
                 TRY(tsl_download(&flag, ovf.p, 4));
             }
@@ -519,13 +528,19 @@ struct Engine {
                 plain = false;
                 TRY(r);
             } else if (out_tok && nwant) {
-                std::copy(dl.begin() + 4, dl.end(), out_tok);
+                std::copy(hout + 4, hout + 4 + nwant, out_tok);
                 return timed ? add_step_time(replayed) : 0;
             }
         }
         if (nwant > 0) {
-            if (out_tok) TRY(tsl_download(out_tok, next.p, nwant * 4));
-            else TRY(tsl_download(out, logits.p, nwant * (size_t)cfg.vocab * 4));
+            if (out_tok) {
+                TRY(rt_download_pinned(hout + 4, next.p, nwant * 4));
+                std::copy(hout + 4, hout + 4 + nwant, out_tok);
+            } else {
+                TRY(tsl_download(out, logits.p, nwant * (size_t)cfg.vocab * 4));
+            }
+        } else {
+            TRY(tsl_sync());  // (the pinned inputs are rewritten by the next step)
         }
         return timed ? add_step_time(replayed) : 0;
     }
@@ -536,7 +551,6 @@ struct Engine {
         timed_ms[replayed ? 0 : 1] += ms;
         return 0;
     }
-    std::vector<int32_t> dl;
 };
 
 std::vector<std::unique_ptr<Engine>> g_engines;
@@ -643,6 +657,8 @@ int tsl_engine_free(int engine) {
         if (b->p) tsl_free(b->p);
     for (auto& L : e->layers)
         for (Buf* b : {&L.n1, &L.wqkv, &L.wo, &L.n2, &L.wg, &L.wu, &L.wd, &L.kc, &L.vc}) tsl_free(b->p);
+    rt_host_free(e->hin);
+    rt_host_free(e->hout);
     g_engines[engine].reset();
     return 0;
 }

@@ -625,3 +625,29 @@ int rt_event_rerecord(int id) {
     CHECK(hipEventRecord(g.events[id], g.stream), "record");
     return 0;
 }
+
+// The engine's per-step transfers through pinned host buffers (library-
+// internal): an upload that is only enqueued (ordered before the step's
+// kernels on the stream; the caller keeps the buffer unchanged until a later
+// synchronisation), and a download that enqueues and waits once.
+int rt_host_alloc(size_t n, void** p) {
+    NEED_OPEN();
+    CHECK(hipHostMalloc(p, n, hipHostMallocDefault), "pinned host buffer");
+    return 0;
+}
+int rt_host_free(void* p) {
+    if (p) CHECK(hipHostFree(p), "pinned host buffer");
+    return 0;
+}
+int rt_upload_async(uint64_t dst, const void* pinned, size_t n) {
+    NEED_OPEN();
+    if (n == 0) return 0;
+    CHECK(hipMemcpyAsync((void*)dst, pinned, n, hipMemcpyHostToDevice, g.stream), "upload");
+    return 0;
+}
+int rt_download_pinned(void* pinned, uint64_t src, size_t n) {
+    NEED_OPEN();
+    if (n) CHECK(hipMemcpyAsync(pinned, (const void*)src, n, hipMemcpyDeviceToHost, g.stream), "download");
+    CHECK(hipStreamSynchronize(g.stream), "download");
+    return 0;
+}
