@@ -450,12 +450,16 @@ def main():
               "(every kernel here runs on one MI355X; the measured value is one GPU's throughput)", file=sys.stderr)
         sys.exit(2)
 
+    only = set(filter(None, args.only.split(",")))
+    if "vendor" in only:
+        import torch  # (initialised before the library opens the device: torch enumerates devices once)
+
+        torch.cuda.init()
     import tessel_amd as T
 
     T.open()
     cus, mhz = T.device_info()
     log("device:", T.device_name(), cus, "CUs", mhz, "MHz")
-    only = set(filter(None, args.only.split(",")))
 
     # ---- headline: GEMM 4096^3
     if args.profile:

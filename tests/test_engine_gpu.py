@@ -230,15 +230,30 @@ def test_tinyllama_shape_against_the_reference(gpu):
 
 def test_tinyllama_full_config_properties(gpu):
     """Config 5 at full size (32 prompts of 512 random ids, 128 greedy
-    steps): packed prefill (two prompts per 1024-token step) and one prompt
-    per step generate the same token streams, graph replay equals eager
-    launches, every request gets 128 tokens (or stops at eos), and the
-    statistics count what ran."""
+    steps): two of the streams token by token against the reference model,
+    packed prefill (two prompts per 1024-token step) and one prompt per step
+    generate the same token streams, graph replay equals eager launches,
+    every request gets 128 tokens (or stops at eos), and the statistics count
+    what ran."""
     cfg, w, e = _tinyllama_engine()
-    del w
     rng = np.random.default_rng(5)
     reqs = [(rng.integers(3, cfg.vocab, 512).tolist(), 128) for _ in range(32)]
     packed, st = e.generate(reqs, 32)
+    # Two of the 32 streams (the first and the last request) against
+    # reference::forward over their whole 639-token histories: every token of
+    # the 32-row decode is the reference's argmax or within 2e-2 of its scale.
+    ocfg = oracle.Config.tinyllama()
+    for k in (0, 31):
+        p, toks = reqs[k][0], packed[k]
+        ref = oracle.forward(ocfg, w, list(p) + toks[:-1])
+        exact = 0
+        for i, t in enumerate(toks):
+            l = ref[len(p) - 1 + i]
+            best = oracle.argmax(l)
+            assert t == best or l[best] - l[t] < 2e-2 * np.abs(l).max(), (k, i, t, best)
+            exact += t == best
+        print(f"config 5 request {k}: {exact} of {len(toks)} tokens the reference's own choice", flush=True)
+    del w
     print(f"config 5: {st.generated} tokens, {st.prefill_steps} prefill + {st.decode_steps} decode steps", flush=True)
     assert st.prefill_steps == 16 and st.prompt_tokens == 32 * 512 and st.largest_batch == 32
     assert st.generated == sum(len(o) for o in packed)
