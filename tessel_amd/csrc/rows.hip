@@ -9,6 +9,7 @@
 #include "common.h"
 
 #include <climits>
+#include <type_traits>
 
 namespace {
 
@@ -34,40 +35,53 @@ __global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ 
     const float* x = X + (size_t)row * C;
     float* y = Y + (size_t)row * C;
     const bool vec = (C % 4) == 0;
-    float v[NV][4];
-    float m = -INFINITY;
+    // FULL: every chunk of every lane lies inside the row (a uniform branch,
+    // so the common shape runs without per-chunk tests).
+    auto body = [&](auto full) {
+        constexpr bool FULL = decltype(full)::value;
+        float v[NV][4];
+        float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int c = i * 256 + lane * 4;
-        if (vec && c + 4 <= ncols) {
-            float4v t = load_once(reinterpret_cast<const float4v*>(x + c));
-            for (int e = 0; e < 4; e++) v[i][e] = t[e];
-        } else {
-            for (int e = 0; e < 4; e++) v[i][e] = (c + e < ncols) ? x[c + e] : -INFINITY;
+        for (int i = 0; i < NV; i++) {
+            const int c = i * 256 + lane * 4;
+            if (FULL || (vec && c + 4 <= ncols)) {
+                float4v t = load_once(reinterpret_cast<const float4v*>(x + c));
+                for (int e = 0; e < 4; e++) v[i][e] = t[e];
+            } else {
+                for (int e = 0; e < 4; e++) v[i][e] = (c + e < ncols) ? x[c + e] : -INFINITY;
+            }
+            for (int e = 0; e < 4; e++) m = fmaxf(m, v[i][e]);
         }
-        for (int e = 0; e < 4; e++) m = fmaxf(m, v[i][e]);
-    }
-    m = wave_max(m);
-    float s = 0.0f;
+        m = wave_max(m);
+        // exp(x - m) as exp2((x - m) log2(e)): one v_exp_f32 and two operations
+        // per element where expf expands to ~12 (its range reduction and
+        // overflow/underflow selects); x - m <= 0, so exp2's argument is in
+        // range, and its rounding adds < 1e-6 relative (the f32 result is
+        // within a few ulp of expf's). 4096^2 from HBM: 25.6 -> 23.8 us.
+        constexpr float LOG2E_F = 1.4426950408889634f;
+        float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NV; i++)
-        for (int e = 0; e < 4; e++) {
-            v[i][e] = expf(v[i][e] - m);
-            s += v[i][e];
-        }
-    const DivBy by_s(wave_sum(s));  // s >= 1: the row's max contributes exp(0)
+        for (int i = 0; i < NV; i++)
+            for (int e = 0; e < 4; e++) {
+                v[i][e] = __builtin_amdgcn_exp2f((v[i][e] - m) * LOG2E_F);
+                s += v[i][e];
+            }
+        const DivBy by_s(wave_sum(s));  // s >= 1: the row's max contributes exp(0)
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int c = i * 256 + lane * 4;
-        if (vec && c + 4 <= ncols) {
-            float4v t;
-            for (int e = 0; e < 4; e++) t[e] = by_s(v[i][e]);
-            store_out(t, reinterpret_cast<float4v*>(y + c));
-        } else {
-            for (int e = 0; e < 4; e++)
-                if (c + e < ncols) y[c + e] = by_s(v[i][e]);
+        for (int i = 0; i < NV; i++) {
+            const int c = i * 256 + lane * 4;
+            if (FULL || (vec && c + 4 <= ncols)) {
+                float4v t;
+                for (int e = 0; e < 4; e++) t[e] = by_s(v[i][e]);
+                store_out(t, reinterpret_cast<float4v*>(y + c));
+            } else {
+                for (int e = 0; e < 4; e++)
+                    if (c + e < ncols) y[c + e] = by_s(v[i][e]);
+            }
         }
-    }
+    };
+    if (vec && ncols == NV * 256) body(std::true_type{});
+    else body(std::false_type{});
 }
 
 // Rows longer than the register tile: a max/sum pass, then the writes.
@@ -95,13 +109,13 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const float* __restri
 // (basic.tl) or f32 (llm.tl); `rows` (rmsnorm_rows) gathers the input row.
 // Writes y[c] = f16(v * rs * w[c]) for this lane's NV chunks of E columns
 // (chunk i starts at column (64 i + lane) E), the first ncols columns only.
-template <int E, int NV>
+template <int E, int NV, bool FULL = false>
 TSL_DEV void rms_store(const float (&v)[NV][E], float rs, const u16* __restrict__ W, u16* __restrict__ y, int lane,
                        int ncols, bool vec) {
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int c = (i * 64 + lane) * E;
-        if (vec && c + E <= ncols) {
+        if (FULL || (vec && c + E <= ncols)) {
             // E outputs: 8 halves (16 bytes) for f16 input rows, 4 (8 bytes) for f32.
             // The weights' E halves in one load (the row's chunk is aligned alike).
             uint32_t wv[E / 2];
