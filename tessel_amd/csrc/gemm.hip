@@ -46,6 +46,17 @@ TSL_DEV int swz(int row, int c) {
 
 enum Epi { EPI_F16 = 0, EPI_F32 = 1, EPI_RESID = 2, EPI_BIAS = 3, EPI_SWIGLU = 4, EPI_ROPE = 5 };
 
+// gate_up's SwiGLU, silu(g) u = g / (1 + exp(-g)) u, for an output rounded
+// to f16: exp as one v_exp_f32 of -g log2(e) and the division as a
+// reciprocal (each within a few f32 ulp of expf / IEEE division, far below
+// the f16 rounding that follows; expf and the division expand to ~20
+// instructions). g -> -inf gives exp2 = inf, a reciprocal of 0 and -0, as
+// the division does.
+TSL_DEV float silu_mul(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
 // The fused QKV projection's epilogue (EPI_ROPE): llm.tl rope_q and kv_write
 // applied to the projection's f16-rounded outputs (column layout of QKV:
 // H query heads, G key heads, G value heads of D columns each).
@@ -233,7 +244,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_f16(const u16* __restri
                     reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
                 } else {
                     const float u = acc2[i][j][r];
-                    reinterpret_cast<u16*>(C)[o] = f2h(v / (1.0f + expf(-v)) * u);
+                    reinterpret_cast<u16*>(C)[o] = f2h(silu_mul(v, u));
                 }
             }
         }
@@ -553,7 +564,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
                     if constexpr (DUAL) pp[mn] = acc2[DUAL ? i : 0][DUAL ? j : 0][r];
                 } else {
                     const float u = acc2[DUAL ? i : 0][DUAL ? j : 0][r];
-                    reinterpret_cast<u16*>(C)[o] = f2h(v / (1.0f + expf(-v)) * u);
+                    reinterpret_cast<u16*>(C)[o] = f2h(silu_mul(v, u));
                 }
             }
         }
@@ -803,7 +814,7 @@ TSL_DEV void sk_store(void* C, const u16* bias, int N, int m, int n, float v, fl
     } else if constexpr (EPI == EPI_BIAS) {
         reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[n]));
     } else {
-        reinterpret_cast<u16*>(C)[o] = f2h(v / (1.0f + expf(-v)) * u);
+        reinterpret_cast<u16*>(C)[o] = f2h(silu_mul(v, u));
     }
 }
 
