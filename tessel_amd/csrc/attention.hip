@@ -109,11 +109,15 @@ __global__ __launch_bounds__(256, (D == 128 && KS == 2) ? 1 : 2) void attn_fwd(A
     const int nqb = (a.S + BQW - 1) / BQW;
     // Work rank (0 = most keys): longest first, and within every full round of
     // NCU workgroups (one per CU) alternately reversed, so the workgroups
-    // sharing a CU (ranks j, 2 NCU-1-j, 2 NCU+j, ...) add up to the same work.
+    // sharing a CU add up to about the same work. The reversal moves whole
+    // groups of 8 ranks (workgroup i runs on XCD i % 8), so with H a multiple
+    // of 8 a head's query blocks all run on one XCD and its K and V are
+    // fetched into one L2 (H32 S4096: 78.6 -> 50.4 MiB read per call).
     int rank = blockIdx.x;
     {
         const int r = rank / a.ncu, j = rank % a.ncu;
-        if ((r & 1) && (r + 1) * a.ncu <= (int)gridDim.x) rank = r * a.ncu + a.ncu - 1 - j;
+        if ((r & 1) && (r + 1) * a.ncu <= (int)gridDim.x)
+            rank = r * a.ncu + (a.ncu % 8 == 0 ? a.ncu - 8 - (j & ~7) + (j & 7) : a.ncu - 1 - j);
     }
     const int qb = nqb - 1 - rank / a.H;
     const int h = rank % a.H;
