@@ -189,6 +189,45 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ X, 
     rms_store<E, NV>(v, rs, W, y, lane, ncols, vec);
 }
 
+// basic.rmsnorm over f16 rows whose every 16-byte chunk is present (ncols ==
+// C == 512 NV): the row and its NV weight chunks stay packed (4 registers a
+// chunk each, not 8 floats), so the weight loads are issued with the row's,
+// before the reduction, and the wavefront waits on one memory round trip
+// instead of two with all 4096 wavefronts of a 4096^2 call resident. Same
+// arithmetic, in the same order, as rmsnorm_kernel.
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_f16_full_kernel(const u16* __restrict__ X, const u16* __restrict__ W,
+                                                               u16* __restrict__ Y, int R, int C, float n, float eps) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * ROWS_PER_WG + (threadIdx.x >> 6);
+    if (row >= R) return;
+    const u16* x = X + (size_t)row * C;
+    u16* y = Y + (size_t)row * C;
+    u32x4 xv[NV], wv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) xv[i] = load_once(reinterpret_cast<const u32x4*>(x + (i * 64 + lane) * 8));
+#pragma unroll
+    for (int i = 0; i < NV; i++) wv[i] = *reinterpret_cast<const u32x4*>(W + (i * 64 + lane) * 8);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+        for (int e = 0; e < 8; e++) {
+            const float v = h2f((u16)(xv[i][e >> 1] >> (16 * (e & 1))));
+            ss += v * v;
+        }
+    ss = wave_sum(ss);
+    const float rs = 1.0f / sqrtf(ss / n + eps);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        u32x4 o;
+        for (int p = 0; p < 4; p++) {
+            const u16 lo = f2h(h2f((u16)(xv[i][p] & 0xffff)) * rs * h2f((u16)(wv[i][p] & 0xffff)));
+            const u16 hi = f2h(h2f((u16)(xv[i][p] >> 16)) * rs * h2f((u16)(wv[i][p] >> 16)));
+            o[p] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        store_out(o, reinterpret_cast<u32x4*>(y + (i * 64 + lane) * 8));
+    }
+}
+
 // ---- one workgroup per row (llm.tl rmsnorm over f32 rows, and the fused
 // residual projection): thread t owns the float4 chunks t, t + 256, ... of
 // the row, so a decode-sized batch (a few dozen rows) still spreads its
@@ -357,6 +396,15 @@ int run_rmsnorm(const XT* X, const int* idx, int xrows, const u16* W, u16* Y, in
         }
     }
     dim3 grid((R + ROWS_PER_WG - 1) / ROWS_PER_WG);
+    if constexpr (sizeof(XT) == 2) {
+        if (!idx && ncols == C && (C == 2048 || C == 4096)) {
+            if (C == 2048)
+                hipLaunchKernelGGL(rmsnorm_f16_full_kernel<4>, grid, dim3(256), 0, s, X, W, Y, R, C, n, eps);
+            else
+                hipLaunchKernelGGL(rmsnorm_f16_full_kernel<8>, grid, dim3(256), 0, s, X, W, Y, R, C, n, eps);
+            return TSL_LAUNCHED(what);
+        }
+    }
     constexpr int E = 16 / sizeof(XT);
     if (ncols <= 64 * E * 4)
         hipLaunchKernelGGL((rmsnorm_kernel<XT, 4>), grid, dim3(256), 0, s, X, idx, xrows, W, Y, R, C, ncols, n, eps);
