@@ -486,7 +486,7 @@ def main():
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_MFMA_F16, 4), "traffic": traffic,
-                     "kernel": "gemm_pp<false, 0> (matmul)", "kernel_ms": round(kern_ms, 5),
+                     "kernel": "gemm_pp16<false, 0> (matmul)", "kernel_ms": round(kern_ms, 5),
                      "algorithmic_per_launch": "2MNK = 137.44 GFLOP"},
         "device": {"name": T.device_name(), "cus": cus, "mhz": mhz},
     }

@@ -756,6 +756,199 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, con
             store_acc32<EPI>(C, bias, M, N, m0 + wm0 + i * 32, n0 + wn0 + j * 32 + (lane & 31), g, acc[i][j]);
 }
 
+// The epilogue of one 16x16 accumulator tile (lane l: column col = .. + l % 16,
+// register r: row row0 + 4 (l / 16) + r) for the plain epilogues.
+template <int EPI>
+TSL_DEV void store_acc16(void* C, const u16* bias, int M, int N, int row0, int col, int g, const float4v& acc) {
+    if (col >= N) return;
+    float old[EPI == EPI_RESID ? 4 : 1];
+    if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = row0 + 4 * g + r;
+            old[r] = row < M ? reinterpret_cast<const float*>(C)[(size_t)row * N + col] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int row = row0 + 4 * g + r;
+        if (row >= M) continue;
+        const size_t o = (size_t)row * N + col;
+        const float v = acc[r];
+        if constexpr (EPI == EPI_F16) {
+            reinterpret_cast<u16*>(C)[o] = f2h(v);
+        } else if constexpr (EPI == EPI_F32) {
+            reinterpret_cast<float*>(C)[o] = v;
+        } else if constexpr (EPI == EPI_RESID) {
+            reinterpret_cast<float*>(C)[o] = old[r] + v;
+        } else if constexpr (EPI == EPI_BIAS) {
+            reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
+        }
+    }
+}
+
+// gemm_pp's ping-pong (256 x 256 tiles, 8 wavefronts of 128 x 64, two
+// groups alternating LDS-read and MFMA phases, same loads and barriers) on
+// v_mfma_f32_16x16x32_f16: the same flops as the 32x32x16 form with a
+// quarter of the accumulator registers read and written per MFMA. On random
+// f16 operands the matrix cores sustain ~1.85 PFLOP/s in this form against
+// ~1.62 in the 32x32x16 form (the clock falls less). Each wavefront holds
+// 8 x 4 tiles of 16 x 16; a 64-k phase is two 32-k substeps of 32 MFMAs.
+// Operands: lane l holds row (A) or column (B) l % 16 and k 8 (l / 16) .. +7
+// of the substep. B [K, N] rows carry the swizzle chunk ^ bsw(k), bsw(k) =
+// 4 (k & 3) + 2 ((k >> 3) & 1): the two 16-lane groups a transposed read
+// serves together (k rows 8 apart, the same 16 columns) land on distinct
+// banks.
+template <bool BT, int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_pp16(const u16* __restrict__ A, const u16* __restrict__ B,
+                                                    void* __restrict__ C, const u16* __restrict__ bias, int M, int N,
+                                                    int K, int G) {
+    constexpr int BM = 256, BN = 256, BK = 64, WGN = 4, KC = BK / 8;
+    constexpr int WM = BM / 2, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
+    constexpr int LP = BM * BK / 512 / 4;
+    constexpr int RPL = 512 / BN, RPA = 512 / BK;
+    constexpr int STAGE = (BM + BN) * BK * 2;
+    constexpr int SUB = 2;  // 32-k substeps per phase
+    __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE / 2];
+    TSL_POISON(lds);
+    auto sw = [](int r) { return (r >> 1) & 7; };
+    auto bsw = [](int k) { return ((k & 3) << 2) | (((k >> 3) & 1) << 1); };
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave >> 2, w4 = wave & 3;
+    const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+    int tm, tn;
+    tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, (N + BN - 1) / BN, G, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int l16 = lane & 15, g16 = lane >> 4;
+    const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
+
+    uint32_t off[LP];
+#pragma unroll
+    for (int i = 0; i < LP; i++) {
+        const int q = w4 * LP + i;
+        if (grp == 0 || BT) {
+            const int r = RPA * q + lane / KC, c = (lane % KC) ^ sw(r);
+            const int lim = grp == 0 ? M - m0 : N - n0, base = grp == 0 ? m0 : n0;
+            off[i] = r < lim ? (uint32_t)(((base + r) * K + 8 * c) * 2) : (uint32_t)OOB;
+        } else {
+            const int rk = RPL * q + lane / (BN / 8), cb = (lane % (BN / 8)) ^ bsw(rk), n = n0 + 8 * cb;
+            off[i] = n < N ? (uint32_t)((rk * N + n) * 2) : (uint32_t)OOB;
+        }
+    }
+    auto issue = [&](int k0, int stage) {
+        const bool a = grp == 0;
+        const long shift = a || BT ? (long)k0 * 2 : (long)k0 * N * 2;
+        const char* base = reinterpret_cast<const char*>(a ? A : B) + shift;
+        i32x4 rs = make_rsrc(base, (uint32_t)((a ? (long)M * K : (long)N * K) * 2 - shift));
+#pragma unroll
+        for (int c = 0; c < 4; c++) rs[c] = __builtin_amdgcn_readfirstlane(rs[c]);
+        const uint32_t dst =
+            __builtin_amdgcn_readfirstlane(lds_base + stage * STAGE + (a ? 0 : BM * BK * 2) + w4 * LP * 1024);
+#pragma unroll
+        for (int i = 0; i < LP; i++)
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(dst + i * 1024),
+                         "v"(off[i]), "s"(rs));
+    };
+
+    // LDS byte addresses (stage 0) of this lane's operands: A tile i at
+    // a_addr[st] + i 16 rows; B tile j at b_addr[j] (+ the substep's k).
+    uint32_t a_addr[SUB], b_addr[TN];
+#pragma unroll
+    for (int st = 0; st < SUB; st++) {
+        const int r = wm0 + l16;
+        a_addr[st] = (uint32_t)((r * KC + ((4 * st + g16) ^ sw(r))) * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        if constexpr (BT) {
+            b_addr[j] = (uint32_t)(BM * BK * 2 + (wn0 + j * 16 + l16) * KC * 16);
+        } else {
+            const int n = wn0 + j * 16 + 4 * (l16 & 3), k = 8 * g16 + (l16 >> 2);
+            b_addr[j] = (uint32_t)(BM * BK * 2 + k * BN * 2 + ((((n >> 3) ^ bsw(k)) << 3) + (n & 7)) * 2);
+        }
+    }
+    const char* ldsc = reinterpret_cast<const char*>(lds);
+    half8 av[SUB][TM], bv[SUB][TN];
+    auto read_step = [&](int stage) {
+        const int so = stage * STAGE;
+#pragma unroll
+        for (int st = 0; st < SUB; st++) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                av[st][i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 16 * BK * 2);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                if constexpr (BT) {
+                    const int r = wn0 + j * 16 + l16;
+                    bv[st][j] = *reinterpret_cast<const half8*>(ldsc + so + b_addr[j] + (((4 * st + g16) ^ sw(r)) * 16));
+                } else {
+                    const u16* p = reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + 32 * st * BN * 2);
+                    bv[st][j] = __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * BN), 0, 1, 2, 3, 4, 5, 6, 7);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    float4v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = float4v{};
+    auto compute = [&]() {
+#pragma unroll
+        for (int u = 0; u < SUB; u++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[u][i], bv[u][j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto bar = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int nk = K / BK;
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    bar();
+    if (grp == 0) {
+        for (int s = 0; s < nk; s++) {
+            if (s + 1 < nk) issue((s + 1) * BK, (s + 1) & 1);
+            read_step(s & 1);
+            bar();
+            compute();
+            __builtin_amdgcn_s_waitcnt(0x0f70);
+            bar();
+        }
+    } else {
+        if (nk > 1) issue(BK, 1);
+        bar();
+        for (int s = 0; s < nk; s++) {
+            read_step(s & 1);
+            if (s + 2 < nk) {
+                issue((s + 2) * BK, s & 1);
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(LP));
+            } else {
+                __builtin_amdgcn_s_waitcnt(0x0f70);
+            }
+            bar();
+            compute();
+            if (s + 1 < nk) bar();
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            store_acc16<EPI>(C, bias, M, N, m0 + wm0 + i * 16, n0 + wn0 + j * 16 + l16, g16, acc[i][j]);
+}
+
 // matmul_f32 (kernels/matmul.tl:19-27): f32 operands through LDS, f32 FMA.
 __global__ __launch_bounds__(256) void matmul_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                          float* __restrict__ C, int M, int N, int K) {
@@ -1671,9 +1864,10 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             // 8 wavefronts of 128 x 64 (2 per SIMD, 128 accumulator registers
             // each): the ping-pong form when K is whole steps, else one
             // wave's MFMAs cover the other's loads and barrier.
+            // (16x16x32 MFMAs: 4096^3 1254-1262 -> 1355-1358 TFLOP/s, 8192^3
+            // 1338-1348 -> 1433-1437 against the 32x32x16 gemm_pp, same box.)
             if (K % 64 == 0)
-                hipLaunchKernelGGL((gemm_pp<BT, EPI, 256, 256, 1>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, C, bias, M, N, K,
-                                   4);
+                hipLaunchKernelGGL((gemm_pp16<BT, EPI>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, C, bias, M, N, K, 4);
             else
                 hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4, 64, 2>), dim3(tiles(256, 256)), dim3(512), 0, s, A,
                                    B, B2, C, bias, M, N, K, 4);
