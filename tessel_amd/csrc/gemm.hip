@@ -570,192 +570,6 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         }
 }
 
-// Large products as a ping-pong of two wavefront groups (K % (64 NH) == 0).
-// 8 wavefronts of (BM/2) x (BN/4) (256 x 256: 128 x 64, as gemm_big's); group
-// 0 (waves 0-3) and group 1 (waves 4-7) put one wavefront on each SIMD and
-// take turns, separated by workgroup barriers: while one group runs a
-// phase's MFMAs back to back from registers, the other reads its next
-// phase's operands from LDS into registers. A phase covers NH steps of 64 k
-// (each stage holds NH halves laid out as gemm_big's 64-k stages, same
-// swizzles), so a phase keeps the matrix cores busy long enough for the
-// other group's reads. Group 0 also loads the A tile of the next phase and
-// group 1 the B tile of the phase after that, so the direct-to-LDS writes
-// are spread over both groups' read phases. Two stages.
-//
-// Phase p (between barriers p and p + 1): group 0 reads step p/2 (p even)
-// or computes step (p-1)/2 (p odd); group 1 is one phase behind. A stage's
-// A (B) tile is rewritten only after both groups' reads of its previous step,
-// and every load has landed (its issuing wave's vmcnt, then a barrier) before
-// the phase that reads it: A of step s + 1 is issued at the start of group
-// 0's read of step s and waited for at the end of its compute of step s; B
-// of step s + 2 is issued by group 1 right after its read of step s and
-// waited for at the end of its read of step s + 1.
-template <bool BT, int EPI, int BM, int BN, int NH>
-__global__ __launch_bounds__(512, 1) void gemm_pp(const u16* __restrict__ A, const u16* __restrict__ B,
-                                                  void* __restrict__ C, const u16* __restrict__ bias, int M, int N,
-                                                  int K, int G) {
-    constexpr int BK = 64, WGN = 4, KC = BK / 8;
-    constexpr int WM = BM / 2, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
-    constexpr int LP = BM * BK / 512 / 4;  // 1 KB loads per wavefront per half (of A in group 0, of B in group 1)
-    static_assert(BM == BN && TM >= 1 && TN >= 1 && (BT || BN >= 128), "tile shape");
-    constexpr int RPL = 512 / BN, RPA = 512 / BK;
-    constexpr int HALF = (BM + BN) * BK * 2;  // bytes of one 64-k half: A [BM][64], then B
-    constexpr int STAGE = NH * HALF;
-    constexpr int SUB = 4 * NH;  // 16-k substeps per phase
-    __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE / 2];
-    TSL_POISON(lds);
-    auto sw = [](int r) { return (r >> 1) & 7; };
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int grp = wave >> 2, w4 = wave & 3;
-    const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
-    int tm, tn;
-    tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, (N + BN - 1) / BN, G, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int g = lane >> 5;
-    const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
-
-    // This wavefront's loads: 1 KB each of the A tile (group 0) or the B
-    // tile (group 1), lane offsets relative to the half's first column (A,
-    // W) or row (B [K, N]); the buffer base advances with k in scalars.
-    uint32_t off[LP];
-#pragma unroll
-    for (int i = 0; i < LP; i++) {
-        const int q = w4 * LP + i;
-        if (grp == 0 || BT) {
-            const int r = RPA * q + lane / KC, c = (lane % KC) ^ sw(r);
-            const int lim = grp == 0 ? M - m0 : N - n0, base = grp == 0 ? m0 : n0;
-            off[i] = r < lim ? (uint32_t)(((base + r) * K + 8 * c) * 2) : (uint32_t)OOB;
-        } else {
-            const int rk = RPL * q + lane / (BN / 8), cb = (lane % (BN / 8)) ^ ((rk & 3) << 2), n = n0 + 8 * cb;
-            off[i] = n < N ? (uint32_t)((rk * N + n) * 2) : (uint32_t)OOB;
-        }
-    }
-    auto issue = [&](int k0, int stage) {
-        const bool a = grp == 0;
-#pragma unroll
-        for (int h = 0; h < NH; h++) {
-            const int k = k0 + BK * h;
-            const long shift = a || BT ? (long)k * 2 : (long)k * N * 2;
-            const char* base = reinterpret_cast<const char*>(a ? A : B) + shift;
-            i32x4 rs = make_rsrc(base, (uint32_t)((a ? (long)M * K : (long)N * K) * 2 - shift));
-#pragma unroll
-            for (int c = 0; c < 4; c++) rs[c] = __builtin_amdgcn_readfirstlane(rs[c]);  // uniform: keep it in SGPRs
-            const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_base + stage * STAGE + h * HALF +
-                                                                (a ? 0 : BM * BK * 2) + w4 * LP * 1024);
-#pragma unroll
-            for (int i = 0; i < LP; i++)
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(dst + i * 1024),
-                             "v"(off[i]), "s"(rs));
-        }
-    };
-
-    // LDS byte addresses of this lane's operands in half 0 of stage 0 (gemm_big's).
-    uint32_t a_addr[BK / 16], b_addr[TN];
-#pragma unroll
-    for (int st = 0; st < BK / 16; st++) {
-        const int r = wm0 + (lane & 31);
-        a_addr[st] = (uint32_t)((r * KC + ((2 * st + g) ^ sw(r))) * 16);
-    }
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-        if constexpr (BT) {
-            b_addr[j] = (uint32_t)(BM * BK * 2 + (wn0 + j * 32 + (lane & 31)) * KC * 16);
-        } else {
-            const int jj = lane & 15;
-            const int n = wn0 + j * 32 + 16 * ((lane >> 4) & 1) + 4 * (jj & 3), k = 8 * g + (jj >> 2);
-            b_addr[j] = (uint32_t)(BM * BK * 2 + k * BN * 2 + ((((n >> 3) ^ ((k & 3) << 2)) << 3) + (n & 7)) * 2);
-        }
-    }
-    const char* ldsc = reinterpret_cast<const char*>(lds);
-    half8 av[SUB][TM], bv[SUB][TN];
-    auto read_step = [&](int stage) {
-#pragma unroll
-        for (int h = 0; h < NH; h++) {
-            const int so = stage * STAGE + h * HALF;
-#pragma unroll
-            for (int st = 0; st < BK / 16; st++) {
-                const int u = 4 * h + st;
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-                    av[u][i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 32 * BK * 2);
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    if constexpr (BT) {
-                        const int r = wn0 + j * 32 + (lane & 31);
-                        bv[u][j] = *reinterpret_cast<const half8*>(ldsc + so + b_addr[j] + (((2 * st + g) ^ sw(r)) * 16));
-                    } else {
-                        const u16* p = reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + 16 * st * BN * 2);
-                        bv[u][j] = __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * BN), 0, 1, 2, 3, 4, 5, 6, 7);
-                    }
-                }
-            }
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the operands are in registers
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    float16v acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = float16v{};
-    auto compute = [&]() {
-#pragma unroll
-        for (int u = 0; u < SUB; u++)
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[u][i], bv[u][j], acc[i][j], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    // A workgroup barrier that nothing is scheduled across (LDS reads and
-    // MFMAs stay in their phase).
-    auto bar = [] {
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_barrier" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-    };
-
-    // Both groups execute 2 nk + 1 barriers.
-    constexpr int PK = BK * NH;  // k per phase
-    const int nk = K / PK;
-    issue(0, 0);
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    bar();
-    if (grp == 0) {
-        for (int s = 0; s < nk; s++) {
-            if (s + 1 < nk) issue((s + 1) * PK, (s + 1) & 1);
-            read_step(s & 1);
-            bar();
-            compute();
-            __builtin_amdgcn_s_waitcnt(0x0f70);  // A of step s + 1 has landed
-            bar();
-        }
-    } else {
-        if (nk > 1) issue(PK, 1);
-        bar();
-        for (int s = 0; s < nk; s++) {
-            read_step(s & 1);
-            if (s + 2 < nk) {
-                issue((s + 2) * PK, s & 1);
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(LP * NH));  // B of step s + 1 has landed
-            } else {
-                __builtin_amdgcn_s_waitcnt(0x0f70);
-            }
-            bar();
-            compute();
-            if (s + 1 < nk) bar();
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-            store_acc32<EPI>(C, bias, M, N, m0 + wm0 + i * 32, n0 + wn0 + j * 32 + (lane & 31), g, acc[i][j]);
-}
-
 // The epilogue of one 16x16 accumulator tile (lane l: column col = .. + l % 16,
 // register r: row row0 + 4 (l / 16) + r) for the plain epilogues.
 template <int EPI>
@@ -787,28 +601,50 @@ TSL_DEV void store_acc16(void* C, const u16* bias, int M, int N, int row0, int c
     }
 }
 
-// gemm_pp's ping-pong (256 x 256 tiles, 8 wavefronts of 128 x 64, two
-// groups alternating LDS-read and MFMA phases, same loads and barriers) on
-// v_mfma_f32_16x16x32_f16: the same flops as the 32x32x16 form with a
-// quarter of the accumulator registers read and written per MFMA. On random
-// f16 operands the matrix cores sustain ~1.85 PFLOP/s in this form against
-// ~1.62 in the 32x32x16 form (the clock falls less). Each wavefront holds
-// 8 x 4 tiles of 16 x 16; a 64-k phase is two 32-k substeps of 32 MFMAs.
-// Operands: lane l holds row (A) or column (B) l % 16 and k 8 (l / 16) .. +7
-// of the substep. B [K, N] rows carry the swizzle chunk ^ bsw(k), bsw(k) =
-// 4 (k & 3) + 2 ((k >> 3) & 1): the two 16-lane groups a transposed read
-// serves together (k rows 8 apart, the same 16 columns) land on distinct
-// banks.
-template <bool BT, int EPI>
+// Large products as a ping-pong of two wavefront groups (K % (64 NH) == 0).
+// 8 wavefronts of (BM/2) x (BN/4) (256 x 256: 128 x 64); group
+// 0 (waves 0-3) and group 1 (waves 4-7) put one wavefront on each SIMD and
+// take turns, separated by workgroup barriers: while one group runs a
+// phase's MFMAs back to back from registers, the other reads its next
+// phase's operands from LDS into registers. A phase covers NH steps of 64 k
+// (each stage holds NH halves laid out as gemm_big's 64-k stages, same
+// swizzles), so a phase keeps the matrix cores busy long enough for the
+// other group's reads. Group 0 also loads the A tile of the next phase and
+// group 1 the B tile of the phase after that, so the direct-to-LDS writes
+// are spread over both groups' read phases. Two stages.
+//
+// Phase p (between barriers p and p + 1): group 0 reads step p/2 (p even)
+// or computes step (p-1)/2 (p odd); group 1 is one phase behind. A stage's
+// A (B) tile is rewritten only after both groups' reads of its previous step,
+// and every load has landed (its issuing wave's vmcnt, then a barrier) before
+// the phase that reads it: A of step s + 1 is issued at the start of group
+// 0's read of step s and waited for at the end of its compute of step s; B
+// of step s + 2 is issued by group 1 right after its read of step s and
+// waited for at the end of its read of step s + 1.
+//
+// The MFMAs are v_mfma_f32_16x16x32_f16: on random f16 operands the matrix
+// cores sustain ~1.85 PFLOP/s in this form against ~1.62 in the 32x32x16
+// form (a quarter of the accumulator registers read and written per MFMA;
+// the clock falls less). Each wavefront holds (WM/16) x (WN/16) tiles of
+// 16 x 16; a 64-k half is two 32-k substeps. Operands: lane l holds row (A)
+// or column (B) l % 16 and k 8 (l / 16) .. +7 of the substep. B [K, N] rows
+// carry the swizzle chunk ^ bsw(k), bsw(k) = 4 (k & 3) + 2 ((k >> 3) & 1):
+// the two 16-lane groups a transposed read serves together (k rows 8 apart,
+// the same 16 columns) land on distinct banks. 4096^3: 1254-1262 -> 1355-1358
+// TFLOP/s, 2048^3 (128 x 128, NH = 2): 737-742 -> 773-775 against the same
+// ping-pong on 32x32x16 MFMAs, same box.
+template <bool BT, int EPI, int BM = 256, int BN = 256, int NH = 1>
 __global__ __launch_bounds__(512, 1) void gemm_pp16(const u16* __restrict__ A, const u16* __restrict__ B,
                                                     void* __restrict__ C, const u16* __restrict__ bias, int M, int N,
                                                     int K, int G) {
-    constexpr int BM = 256, BN = 256, BK = 64, WGN = 4, KC = BK / 8;
+    constexpr int BK = 64, WGN = 4, KC = BK / 8;
     constexpr int WM = BM / 2, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
     constexpr int LP = BM * BK / 512 / 4;
+    static_assert(BM == BN && TM >= 1 && TN >= 1 && (BT || BN >= 128), "tile shape");
     constexpr int RPL = 512 / BN, RPA = 512 / BK;
-    constexpr int STAGE = (BM + BN) * BK * 2;
-    constexpr int SUB = 2;  // 32-k substeps per phase
+    constexpr int HALF = (BM + BN) * BK * 2;  // bytes of one 64-k half: A [BM][64], then B
+    constexpr int STAGE = NH * HALF;
+    constexpr int SUB = 2 * NH;  // 32-k substeps per phase
     __shared__ __attribute__((aligned(16))) u16 lds[2 * STAGE / 2];
     TSL_POISON(lds);
     auto sw = [](int r) { return (r >> 1) & 7; };
@@ -839,24 +675,28 @@ __global__ __launch_bounds__(512, 1) void gemm_pp16(const u16* __restrict__ A, c
     }
     auto issue = [&](int k0, int stage) {
         const bool a = grp == 0;
-        const long shift = a || BT ? (long)k0 * 2 : (long)k0 * N * 2;
-        const char* base = reinterpret_cast<const char*>(a ? A : B) + shift;
-        i32x4 rs = make_rsrc(base, (uint32_t)((a ? (long)M * K : (long)N * K) * 2 - shift));
 #pragma unroll
-        for (int c = 0; c < 4; c++) rs[c] = __builtin_amdgcn_readfirstlane(rs[c]);
-        const uint32_t dst =
-            __builtin_amdgcn_readfirstlane(lds_base + stage * STAGE + (a ? 0 : BM * BK * 2) + w4 * LP * 1024);
+        for (int h = 0; h < NH; h++) {
+            const int k = k0 + BK * h;
+            const long shift = a || BT ? (long)k * 2 : (long)k * N * 2;
+            const char* base = reinterpret_cast<const char*>(a ? A : B) + shift;
+            i32x4 rs = make_rsrc(base, (uint32_t)((a ? (long)M * K : (long)N * K) * 2 - shift));
 #pragma unroll
-        for (int i = 0; i < LP; i++)
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(dst + i * 1024),
-                         "v"(off[i]), "s"(rs));
+            for (int c = 0; c < 4; c++) rs[c] = __builtin_amdgcn_readfirstlane(rs[c]);
+            const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_base + stage * STAGE + h * HALF +
+                                                                (a ? 0 : BM * BK * 2) + w4 * LP * 1024);
+#pragma unroll
+            for (int i = 0; i < LP; i++)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(dst + i * 1024),
+                             "v"(off[i]), "s"(rs));
+        }
     };
 
     // LDS byte addresses (stage 0) of this lane's operands: A tile i at
     // a_addr[st] + i 16 rows; B tile j at b_addr[j] (+ the substep's k).
-    uint32_t a_addr[SUB], b_addr[TN];
+    uint32_t a_addr[2], b_addr[TN];
 #pragma unroll
-    for (int st = 0; st < SUB; st++) {
+    for (int st = 0; st < 2; st++) {
         const int r = wm0 + l16;
         a_addr[st] = (uint32_t)((r * KC + ((4 * st + g16) ^ sw(r))) * 16);
     }
@@ -872,20 +712,20 @@ __global__ __launch_bounds__(512, 1) void gemm_pp16(const u16* __restrict__ A, c
     const char* ldsc = reinterpret_cast<const char*>(lds);
     half8 av[SUB][TM], bv[SUB][TN];
     auto read_step = [&](int stage) {
-        const int so = stage * STAGE;
 #pragma unroll
-        for (int st = 0; st < SUB; st++) {
+        for (int u = 0; u < SUB; u++) {
+            const int so = stage * STAGE + (u >> 1) * HALF, st = u & 1;
 #pragma unroll
             for (int i = 0; i < TM; i++)
-                av[st][i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 16 * BK * 2);
+                av[u][i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 16 * BK * 2);
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 if constexpr (BT) {
                     const int r = wn0 + j * 16 + l16;
-                    bv[st][j] = *reinterpret_cast<const half8*>(ldsc + so + b_addr[j] + (((4 * st + g16) ^ sw(r)) * 16));
+                    bv[u][j] = *reinterpret_cast<const half8*>(ldsc + so + b_addr[j] + (((4 * st + g16) ^ sw(r)) * 16));
                 } else {
                     const u16* p = reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + 32 * st * BN * 2);
-                    bv[st][j] = __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * BN), 0, 1, 2, 3, 4, 5, 6, 7);
+                    bv[u][j] = __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * BN), 0, 1, 2, 3, 4, 5, 6, 7);
                 }
             }
         }
@@ -913,13 +753,14 @@ __global__ __launch_bounds__(512, 1) void gemm_pp16(const u16* __restrict__ A, c
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    const int nk = K / BK;
+    constexpr int PK = BK * NH;  // k per phase
+    const int nk = K / PK;
     issue(0, 0);
     __builtin_amdgcn_s_waitcnt(0x0f70);
     bar();
     if (grp == 0) {
         for (int s = 0; s < nk; s++) {
-            if (s + 1 < nk) issue((s + 1) * BK, (s + 1) & 1);
+            if (s + 1 < nk) issue((s + 1) * PK, (s + 1) & 1);
             read_step(s & 1);
             bar();
             compute();
@@ -927,13 +768,13 @@ __global__ __launch_bounds__(512, 1) void gemm_pp16(const u16* __restrict__ A, c
             bar();
         }
     } else {
-        if (nk > 1) issue(BK, 1);
+        if (nk > 1) issue(PK, 1);
         bar();
         for (int s = 0; s < nk; s++) {
             read_step(s & 1);
             if (s + 2 < nk) {
-                issue((s + 2) * BK, s & 1);
-                __builtin_amdgcn_s_waitcnt(vmcnt_imm(LP));
+                issue((s + 2) * PK, s & 1);
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(LP * NH));
             } else {
                 __builtin_amdgcn_s_waitcnt(0x0f70);
             }
@@ -1864,8 +1705,6 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             // 8 wavefronts of 128 x 64 (2 per SIMD, 128 accumulator registers
             // each): the ping-pong form when K is whole steps, else one
             // wave's MFMAs cover the other's loads and barrier.
-            // (16x16x32 MFMAs: 4096^3 1254-1262 -> 1355-1358 TFLOP/s, 8192^3
-            // 1338-1348 -> 1433-1437 against the 32x32x16 gemm_pp, same box.)
             if (K % 64 == 0)
                 hipLaunchKernelGGL((gemm_pp16<BT, EPI>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, C, bias, M, N, K, 4);
             else
@@ -1909,7 +1748,7 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             // 25.7 -> 24.8 us), else 3 stages (30.0 -> 26.5 us against 4
             // wavefronts, 2 stages).
             if (K % 128 == 0)
-                hipLaunchKernelGGL((gemm_pp<BT, EPI, 128, 128, 2>), dim3(tiles(128, 128)), dim3(512), 0, s, A, B, C, bias,
+                hipLaunchKernelGGL((gemm_pp16<BT, EPI, 128, 128, 2>), dim3(tiles(128, 128)), dim3(512), 0, s, A, B, C, bias,
                                    M, N, K, 4);
             else
                 hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 4, 64, 3>), dim3(tiles(128, 128)), dim3(512), 0, s, A,
