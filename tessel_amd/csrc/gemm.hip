@@ -15,6 +15,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 bool reduce_rmsnorm_fits(int C);
 int run_reduce_rmsnorm(const float* part, int S, float* R, const u16* W, u16* Y, int M, int C, float eps,
@@ -319,6 +320,37 @@ TSL_DEV void store_acc32(void* C, const u16* bias, int M, int N, int row0, int c
     }
 }
 
+// The epilogue of one 16x16 accumulator tile (lane l: column col = .. + l % 16,
+// register r: row row0 + 4 (l / 16) + r) for the plain epilogues.
+template <int EPI>
+TSL_DEV void store_acc16(void* C, const u16* bias, int M, int N, int row0, int col, int g, const float4v& acc) {
+    if (col >= N) return;
+    float old[EPI == EPI_RESID ? 4 : 1];
+    if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = row0 + 4 * g + r;
+            old[r] = row < M ? reinterpret_cast<const float*>(C)[(size_t)row * N + col] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int row = row0 + 4 * g + r;
+        if (row >= M) continue;
+        const size_t o = (size_t)row * N + col;
+        const float v = acc[r];
+        if constexpr (EPI == EPI_F16) {
+            reinterpret_cast<u16*>(C)[o] = f2h(v);
+        } else if constexpr (EPI == EPI_F32) {
+            reinterpret_cast<float*>(C)[o] = v;
+        } else if constexpr (EPI == EPI_RESID) {
+            reinterpret_cast<float*>(C)[o] = old[r] + v;
+        } else if constexpr (EPI == EPI_BIAS) {
+            reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
+        }
+    }
+}
+
 // The compute of a K step is software pipelined: the MFMA operands of
 // k-step s+1 are read from LDS while the 16 MFMAs of step s run.
 //
@@ -333,7 +365,7 @@ TSL_DEV void store_acc32(void* C, const u16* bias, int M, int N, int row0, int c
 // slices of the K steps and leaves its f32 sums in part[ks][p][m][n] (p: gate,
 // up) for skinny_reduce, which adds the slices in order and applies the
 // epilogue.
-template <bool BT, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS, bool SPLIT = false>
+template <bool BT, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS, bool SPLIT = false, bool M16 = false>
 __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restrict__ A, const u16* __restrict__ B,
                                                              const u16* __restrict__ B2, void* __restrict__ C,
                                                              const u16* __restrict__ bias, int M, int N, int K,
@@ -342,7 +374,17 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     static_assert((BK == 64 || BK == 32) && NS >= 2 && NS <= 4, "k step and stages");
     constexpr int NW = WGM * WGN;                 // wavefronts: WGM x WGN, each (BM/WGM) x (BN/WGN)
     constexpr int WM = BM / WGM, WN = BN / WGN;
-    constexpr int TM = WM / 32, TN = WN / 32;     // 32x32 MFMA tiles per wave
+    // M16 (every launch): v_mfma_f32_16x16x32_f16 on 16 x 16 tiles (lane l: row
+    // / column l % 16, k 8 (l / 16) .. +7 of a 32-k substep; gemm_pp16's layout
+    // and B swizzle), which the matrix cores sustain at a higher clock on
+    // random data (prefill-sized products: down 1024x2048x5632 41.8 -> 39.7 us,
+    // gate_up 1024x5632x2048 50.7 -> 48.6, qkv 21.6 -> 21.1). Else the
+    // v_mfma_f32_32x32x16_f16 form on 32 x 32 tiles (16-k substeps), the
+    // layout the swizzles above describe.
+    constexpr int MT = M16 ? 16 : 32;             // MFMA tile edge
+    constexpr int TM = WM / MT, TN = WN / MT;     // MFMA tiles per wave
+    constexpr int KSUB = M16 ? 32 : 16, NSUB = BK / KSUB;  // k per substep, substeps per K step
+    typedef std::conditional_t<M16, float4v, float16v> AccT;
     constexpr int LPA = BM * BK / 512 / NW, LPB = BN * BK / 512 / NW;  // 1 KB loads per wave per K step
     constexpr int RPL = 512 / BN;                 // B [K, N] rows per 1 KB load
     constexpr int RPA = 512 / BK;                 // A (W) rows per 1 KB load
@@ -355,6 +397,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     TSL_POISON(lds);
     // Row r of an A (W) tile holds logical 16-byte chunk c at c ^ sw(r).
     auto sw = [](int r) { return KC == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
+    auto bsw = [](int k) { return M16 ? ((k & 3) << 2) | (((k >> 3) & 1) << 1) : (k & 3) << 2; };  // B [K, N] rows
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -389,7 +432,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
             offb[i] = n0 + r < N ? (uint32_t)(((n0 + r) * K + 8 * c) * 2) : (uint32_t)OOB;
         } else {
             const int rk = RPL * q + lane / (BN / 8);  // k row of the step
-            const int cb = (lane % (BN / 8)) ^ ((rk & 3) << 2);
+            const int cb = (lane % (BN / 8)) ^ bsw(rk);
             const int n = n0 + 8 * cb;
             kb[i] = rk;
             offb[i] = n < N ? (uint32_t)((rk * N + n) * 2) : (uint32_t)OOB;
@@ -439,53 +482,59 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
 
     // LDS byte addresses of this lane's operands in stage 0: A at k-step s,
     // tile i: a_addr[s] + 4096 i; B (NN) tile j: b_addr[j] + (16 s + 4 h) 512.
-    uint32_t a_addr[BK / 16], b_addr[TN];
+    const int l16 = lane & 15, g16 = lane >> 4;
+    const int lr = M16 ? l16 : (lane & 31), kg = M16 ? g16 : g;  // operand row / column in the tile, k group
+    uint32_t a_addr[NSUB], b_addr[TN];
 #pragma unroll
-    for (int st = 0; st < BK / 16; st++) {
-        const int r = wm0 + (lane & 31);
-        a_addr[st] = (uint32_t)((r * KC + ((2 * st + g) ^ sw(r))) * 16);
+    for (int st = 0; st < NSUB; st++) {
+        const int r = wm0 + lr;
+        a_addr[st] = (uint32_t)((r * KC + (((M16 ? 4 : 2) * st + kg) ^ sw(r))) * 16);
     }
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         if constexpr (BT) {
-            const int r = wn0 + j * 32 + (lane & 31);
+            const int r = wn0 + j * MT + lr;
             b_addr[j] = (uint32_t)(BM * BK * 2 + r * KC * 16);
         } else {
             const int grp = lane >> 4, jj = lane & 15;
-            const int n = wn0 + j * 32 + 16 * (grp & 1) + 4 * (jj & 3);
-            const int k = 8 * g + (jj >> 2);
-            b_addr[j] = (uint32_t)(BM * BK * 2 + k * BN * 2 + ((((n >> 3) ^ ((k & 3) << 2)) << 3) + (n & 7)) * 2);
+            const int n = M16 ? wn0 + j * 16 + 4 * (jj & 3) : wn0 + j * 32 + 16 * (grp & 1) + 4 * (jj & 3);
+            const int k = (M16 ? 8 * g16 : 8 * g) + (jj >> 2);
+            b_addr[j] = (uint32_t)(BM * BK * 2 + k * BN * 2 + ((((n >> 3) ^ bsw(k)) << 3) + (n & 7)) * 2);
         }
     }
     const char* ldsc = reinterpret_cast<const char*>(lds);
     auto read_ops = [&](int so, int st, half8* av, half8* bv, half8* bv2) {
 #pragma unroll
-        for (int i = 0; i < TM; i++) av[i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * 32 * BK * 2);
+        for (int i = 0; i < TM; i++) av[i] = *reinterpret_cast<const half8*>(ldsc + so + a_addr[st] + i * MT * BK * 2);
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             if constexpr (BT) {
-                const int r = wn0 + j * 32 + (lane & 31);
-                const int cb = so + b_addr[j] + (((2 * st + g) ^ sw(r)) * 16);
+                const int r = wn0 + j * MT + lr;
+                const int cb = so + b_addr[j] + ((((M16 ? 4 : 2) * st + kg) ^ sw(r)) * 16);
                 bv[j] = *reinterpret_cast<const half8*>(ldsc + cb);
                 if constexpr (DUAL) bv2[j] = *reinterpret_cast<const half8*>(ldsc + cb + BB);
             } else {
-                const half4 h0 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + (16 * st) * BN * 2));
-                const half4 h1 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + (16 * st + 4) * BN * 2));
+                const half4 h0 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + (KSUB * st) * BN * 2));
+                const half4 h1 = lds_read_tr(reinterpret_cast<const u16*>(ldsc + so + b_addr[j] + (KSUB * st + 4) * BN * 2));
                 bv[j] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
             }
         }
     };
 
-    float16v acc[TM][TN], acc2[DUAL ? TM : 1][DUAL ? TN : 1];
+    AccT acc[TM][TN], acc2[DUAL ? TM : 1][DUAL ? TN : 1];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = float16v{};
+        for (int j = 0; j < TN; j++) acc[i][j] = AccT{};
     if constexpr (DUAL)
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++) acc2[i][j] = float16v{};
+            for (int j = 0; j < TN; j++) acc2[i][j] = AccT{};
+    auto mfma = [](const half8& x, const half8& y, const AccT& c) {
+        if constexpr (M16) return __builtin_amdgcn_mfma_f32_16x16x32_f16(x, y, c, 0, 0, 0);
+        else return __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, c, 0, 0, 0);
+    };
 
     // NS stages in a ring, NS - 1 k steps in flight: iteration kt waits for
     // step kt (this wave's loads of later steps may still run), syncs (every
@@ -507,18 +556,17 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         stage = stage + 1 == NS ? 0 : stage + 1;
         read_ops(so, 0, a0, b0, c0);
 #pragma unroll
-        for (int st = 0; st < BK / 16; st++) {
+        for (int st = 0; st < NSUB; st++) {
             half8* av = (st & 1) ? a1 : a0;
             half8* bv = (st & 1) ? b1 : b0;
             half8* cv = (st & 1) ? c1 : c0;
-            if (st + 1 < BK / 16) read_ops(so, st + 1, (st & 1) ? a0 : a1, (st & 1) ? b0 : b1, (st & 1) ? c0 : c1);
+            if (st + 1 < NSUB) read_ops(so, st + 1, (st & 1) ? a0 : a1, (st & 1) ? b0 : b1, (st & 1) ? c0 : c1);
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
-                    if constexpr (DUAL)
-                        acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], cv[j], acc2[i][j], 0, 0, 0);
+                    acc[i][j] = mfma(av[i], bv[j], acc[i][j]);
+                    if constexpr (DUAL) acc2[i][j] = mfma(av[i], cv[j], acc2[i][j]);
                 }
         }
         // Pin the schedule: step 0's operand reads, then per k-step the next
@@ -527,8 +575,8 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         constexpr int NMF = (DUAL ? 2 : 1) * TM * TN;                    // MFMAs per k-step
         __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
 #pragma unroll
-        for (int st = 0; st < BK / 16; st++) {
-            if (st + 1 < BK / 16) {
+        for (int st = 0; st < NSUB; st++) {
+            if (st + 1 < NSUB) {
 #pragma unroll
                 for (int t = 0; t < NRD / 2; t++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -545,15 +593,16 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const int row0 = m0 + wm0 + i * 32, col = n0 + wn0 + j * 32 + (lane & 31);
+            const int row0 = m0 + wm0 + i * MT, col = n0 + wn0 + j * MT + lr;
             if constexpr (!SPLIT && !DUAL) {
-                store_acc32<EPI>(C, bias, M, N, row0, col, g, acc[i][j]);
+                if constexpr (M16) store_acc16<EPI>(C, bias, M, N, row0, col, g16, acc[i][j]);
+                else store_acc32<EPI>(C, bias, M, N, row0, col, g, acc[i][j]);
                 continue;
             }
             if (col >= N) continue;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = row0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            for (int r = 0; r < (M16 ? 4 : 16); r++) {
+                const int row = M16 ? row0 + 4 * g16 + r : row0 + 8 * (r >> 2) + 4 * g + (r & 3);
                 if (row >= M) continue;
                 const size_t o = (size_t)row * N + col;
                 const float v = acc[i][j][r];
@@ -568,37 +617,6 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
                 }
             }
         }
-}
-
-// The epilogue of one 16x16 accumulator tile (lane l: column col = .. + l % 16,
-// register r: row row0 + 4 (l / 16) + r) for the plain epilogues.
-template <int EPI>
-TSL_DEV void store_acc16(void* C, const u16* bias, int M, int N, int row0, int col, int g, const float4v& acc) {
-    if (col >= N) return;
-    float old[EPI == EPI_RESID ? 4 : 1];
-    if constexpr (EPI == EPI_RESID) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int row = row0 + 4 * g + r;
-            old[r] = row < M ? reinterpret_cast<const float*>(C)[(size_t)row * N + col] : 0.0f;
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int row = row0 + 4 * g + r;
-        if (row >= M) continue;
-        const size_t o = (size_t)row * N + col;
-        const float v = acc[r];
-        if constexpr (EPI == EPI_F16) {
-            reinterpret_cast<u16*>(C)[o] = f2h(v);
-        } else if constexpr (EPI == EPI_F32) {
-            reinterpret_cast<float*>(C)[o] = v;
-        } else if constexpr (EPI == EPI_RESID) {
-            reinterpret_cast<float*>(C)[o] = old[r] + v;
-        } else if constexpr (EPI == EPI_BIAS) {
-            reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
-        }
-    }
 }
 
 // Large products as a ping-pong of two wavefront groups (K % (64 NH) == 0).
@@ -1708,7 +1726,7 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             if (K % 64 == 0)
                 hipLaunchKernelGGL((gemm_pp16<BT, EPI>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, C, bias, M, N, K, 4);
             else
-                hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4, 64, 2>), dim3(tiles(256, 256)), dim3(512), 0, s, A,
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4, 64, 2, false, true>), dim3(tiles(256, 256)), dim3(512), 0, s, A,
                                    B, B2, C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
@@ -1718,7 +1736,7 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             // 8 wavefronts of 64 x 64 x (gate, up): the 256 x 256 tile's
             // register budget, and half the workgroups of 128 x 128 tiles, so
             // prefill-sized products (M ~ 1024) fill the CUs in one round.
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 128, 4, 2, 64, 2>), dim3(tiles(256, 128)), dim3(512), 0, s, A, B, B2,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 128, 4, 2, 64, 2, false, true>), dim3(tiles(256, 128)), dim3(512), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
@@ -1729,7 +1747,7 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             // 64 x 64 tiles of 4 wavefronts and 3 stages fill every CU without
             // a K split. 1024 x 2048 x 2048: 23.8 -> 18.7 us; x 5632 (split
             // 2 + reduce before): 47.4 -> 42.8; 1024 x 2560 x 2048: 23.0 -> 22.1.
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 64, 2, 2, 64, 3>), dim3(tiles(64, 64)), dim3(256), 0, s, A, B, B2, C,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 64, 2, 2, 64, 3, false, true>), dim3(tiles(64, 64)), dim3(256), 0, s, A, B, B2, C,
                                bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
@@ -1737,7 +1755,7 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
     if (aligned && M > 64 && (BT || !DUAL)) {
         const int split = part ? big_split(M, N, K) : 1;
         if (split > 1) {  // 128 x 128 tiles over K slices, then the ordered sum
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2, true>), dim3(tiles(128, 128), split), dim3(256), 0, s, A,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2, true, true>), dim3(tiles(128, 128), split), dim3(256), 0, s, A,
                                B, B2, C, bias, M, N, K, 4, part);
             const long mn = (long)M * N;
             hipLaunchKernelGGL(skinny_reduce<EPI>, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, split, M,
@@ -1751,20 +1769,20 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
                 hipLaunchKernelGGL((gemm_pp16<BT, EPI, 128, 128, 2>), dim3(tiles(128, 128)), dim3(512), 0, s, A, B, C, bias,
                                    M, N, K, 4);
             else
-                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 4, 64, 3>), dim3(tiles(128, 128)), dim3(512), 0, s, A,
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 4, 64, 3, false, true>), dim3(tiles(128, 128)), dim3(512), 0, s, A,
                                    B, B2, C, bias, M, N, K, 4);
         } else if (tiles(128, 128) >= 256) {
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2, false, true>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
         } else if (!BT && tiles(64, 128) < 256 && tiles(32, 128) >= 256) {
             // matmul with too few 64 x 128 tiles to fill the CUs (1024^3):
             // 32 x 128 tiles, 4 wavefronts of 32 x 32 (9.05 -> 7.95 us).
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 32, 128, 1, 4, 64, 2>), dim3(tiles(32, 128)), dim3(256), 0, s, A, B, B2,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 32, 128, 1, 4, 64, 2, false, true>), dim3(tiles(32, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
         } else {  // 64 x 128 tiles (4 wavefronts of 64 x 32): twice the workgroups;
                   // X W^T keeps two K steps in flight (matmul's in-register B
                   // transpose does better with one)
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 128, 1, 4, 64, BT ? 3 : 2>), dim3(tiles(64, 128)), dim3(256), 0, s, A,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 128, 1, 4, 64, BT ? 3 : 2, false, true>), dim3(tiles(64, 128)), dim3(256), 0, s, A,
                                B, B2, C, bias, M, N, K, 4);
         }
         return TSL_LAUNCHED(what);
@@ -1861,7 +1879,7 @@ int launch_linear_residual_rmsnorm(TslKernel& k, const uint64_t* a, hipStream_t 
     const int bsplit = k.scratch && aligned && M > 64 && tiles256 < 224 ? big_split(M, N, K) : 1;
     if (bsplit > 1 && ncols == N && reduce_rmsnorm_fits(N)) {
         const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
-        hipLaunchKernelGGL((gemm_big<true, EPI_RESID, 128, 128, 2, 2, 64, 2, true>), dim3(tiles, bsplit), dim3(256), 0, s,
+        hipLaunchKernelGGL((gemm_big<true, EPI_RESID, 128, 128, 2, 2, 64, 2, true, true>), dim3(tiles, bsplit), dim3(256), 0, s,
                            P<u16>(a[0]), P<u16>(a[1]), nullptr, R, nullptr, M, N, K, 4,
                            reinterpret_cast<float*>(k.scratch));
         if (int e = TSL_LAUNCHED("linear_residual_rmsnorm")) return e;
