@@ -567,6 +567,11 @@ def main():
                     cases.append({"case": "probe: mfma 32x32x16 f16, " + ("random" if rnd else "near-constant") +
                                   " operands" + (", with the GEMM's LDS operand reads" if reads else ""),
                                   "tflops": round(tf, 1), "frac_mfma": round(tf / PEAK_MFMA_F16, 4)})
+            for rnd in (False, True):
+                tf = T.probe_mfma16(rnd)
+                cases.append({"case": "probe: mfma 16x16x32 f16 (the GEMMs' form), " +
+                                      ("random" if rnd else "near-constant") + " operands, registers only",
+                              "tflops": round(tf, 1), "frac_mfma": round(tf / PEAK_MFMA_F16, 4)})
             big = T.alloc(1 << 30)
             T.write(big, 0, np.ones(1 << 28, np.float32))
             for mb in (10, 23, 46, 131, 512):

@@ -135,6 +135,9 @@ int tsl_decode_attention_noalloc(uint64_t q, uint64_t kc, uint64_t vc, uint64_t 
  * or without the GEMM's LDS operand reads (lds_reads = 1). One launch of
  * iters iterations after a warm-up launch. */
 int tsl_probe_mfma(int random, int lds_reads, int iters, double* tflops);
+/* The same with v_mfma_f32_16x16x32_f16 (8 independent 16x16 accumulators
+ * per wave, operands in registers): the MFMA form the GEMMs use. */
+int tsl_probe_mfma16(int random, int iters, double* tflops);
 /* GB/s of iters back-to-back streaming reads of bytes each (512 workgroups,
  * four 16-byte loads in flight per lane), launch i reading window i (mod the
  * windows that fit) of the buf_bytes at device address buf. */

@@ -51,7 +51,7 @@ EXPORTS = [
     "tsl_engine_set", "tsl_engine_step", "tsl_generate", "tsl_checkpoint_config", "tsl_checkpoint_load",
     "tsl_checkpoint_save", "tsl_json_roundtrip", "tsl_rng_new", "tsl_rng_bits", "tsl_rng_tensor",
     "tsl_time_each", "tsl_engine_profile", "tsl_engine_profile_rows", "tsl_schedule_trace",
-    "tsl_graph_nodes", "tsl_engine_graphs", "tsl_engine_fallbacks", "tsl_engine_step_times", "tsl_probe_mfma", "tsl_probe_stream",
+    "tsl_graph_nodes", "tsl_engine_graphs", "tsl_engine_fallbacks", "tsl_engine_step_times", "tsl_probe_mfma", "tsl_probe_mfma16", "tsl_probe_stream",
     "tsl_decode_attention_noalloc",
 ]
 
@@ -119,6 +119,7 @@ def _declare(L):
     L.tsl_generate.argtypes = [_INT, _INT, _P, _P, _P, _INT, _INT, _P, _P, ctypes.POINTER(Stats), _P]
     L.tsl_graph_nodes.argtypes = [_INT, _P]
     L.tsl_probe_mfma.argtypes = [_INT, _INT, _INT, ctypes.POINTER(ctypes.c_double)]
+    L.tsl_probe_mfma16.argtypes = [_INT, _INT, ctypes.POINTER(ctypes.c_double)]
     L.tsl_probe_stream.argtypes = [_U64, ctypes.c_size_t, ctypes.c_size_t, _INT, ctypes.POINTER(ctypes.c_double)]
     L.tsl_engine_graphs.argtypes = [_INT, _P, _P, _INT, ctypes.POINTER(_INT)]
     L.tsl_engine_fallbacks.argtypes = [_INT, ctypes.POINTER(_I64)]
@@ -327,6 +328,14 @@ def probe_mfma(random, lds_reads, iters=2000):
     without the GEMM's LDS operand reads)."""
     v = ctypes.c_double()
     check(lib().tsl_probe_mfma(int(random), int(lds_reads), int(iters), ctypes.byref(v)))
+    return v.value
+
+
+def probe_mfma16(random, iters=2000):
+    """TFLOP/s the matrix cores sustain on v_mfma_f32_16x16x32_f16 from
+    registers (the GEMMs' MFMA form), random or nearly constant f16 operands."""
+    v = ctypes.c_double()
+    check(lib().tsl_probe_mfma16(int(random), int(iters), ctypes.byref(v)))
     return v.value
 
 

@@ -8,6 +8,10 @@
 //                     either constant-like (few toggling bits) or random f16,
 //                     optionally with the GEMM's per-k-step LDS operand reads
 //                     (4 ds_read_b128 + 4 ds_read_b64_tr_b16 per 8 MFMAs)
+//   tsl_probe_mfma16  the same with v_mfma_f32_16x16x32_f16 (8 independent
+//                     16x16 accumulators per wave, registers only): the form
+//                     the GEMMs use, whose operand and accumulator traffic
+//                     per flop lets the clock fall less on random data
 //   tsl_probe_stream  streaming reads by 512 workgroups, four 16-byte loads
 //                     in flight per lane, each launch a new window of a large
 //                     buffer: the HBM floor (launch included) of a kernel
@@ -99,6 +103,44 @@ __global__ __launch_bounds__(512, 1) void probe_mfma_kernel(float* out, int n) {
     out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// v_mfma_f32_16x16x32_f16 back to back from registers, 8 independent 16 x 16
+// accumulators per wave, 8 waves per CU, a workgroup barrier every 32 MFMAs.
+template <bool RANDOM>
+__global__ __launch_bounds__(512, 1) void probe_mfma16_kernel(float* out, int n) {
+    const int lane = threadIdx.x & 63;
+    half8 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            uint32_t h = (uint32_t)(lane * 97 + i * 13 + e * 7 + blockIdx.x * 31 + threadIdx.x) * 2654435761u;
+            h ^= h >> 15;
+            h *= 0x5bd1e995u;
+            h ^= h >> 13;
+            a[i][e] = RANDOM ? (half_t)(((int)(h & 0xffff) - 32768) * (1.0f / 16384.0f)) : (half_t)(1e-3f * (e & 7));
+            b[i][e] = RANDOM ? (half_t)(((int)(h >> 16) - 32768) * (1.0f / 16384.0f)) : (half_t)(1e-3f * (i & 7));
+        }
+    float4v acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = float4v{};
+    for (int it = 0; it < n; it++) {
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i * 2 + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[(i + st) & 3], b[(j + st) & 3], acc[i * 2 + j], 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) s += acc[i][r];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
 __global__ __launch_bounds__(512) void probe_stream_kernel(const u32x4* __restrict__ p, size_t n16,
                                                            uint32_t* __restrict__ out) {
     constexpr int U = 4;
@@ -155,6 +197,26 @@ extern "C" int tsl_probe_mfma(int random, int lds_reads, int iters, double* tflo
     // 8 MFMAs of 32x32x16 (2 x 16384 flops each) per wave per k-step quarter,
     // 4 quarters per iteration, 8 waves per CU.
     *tflops = 2.0 * 32 * 32 * 16 * 8 * 4 * 8 * (double)cus * iters / (ms * 1e-3) / 1e12;
+    return 0;
+}
+
+extern "C" int tsl_probe_mfma16(int random, int iters, double* tflops) {
+    if (iters <= 0 || iters > 1 << 20) return tsl_fail(TSL_ERR_ARG, "probe_mfma16: iters in 1 .. 2^20");
+    if (tsl_open()) return -1;
+    const int cus = num_cus();
+    float* out = nullptr;
+    if (tsl_hip_check(hipMalloc(&out, (size_t)cus * 512 * 4), "probe_mfma16 buffer")) return -1;
+    auto go = [&](hipStream_t s) {
+        if (random) hipLaunchKernelGGL(probe_mfma16_kernel<true>, dim3(cus), dim3(512), 0, s, out, iters);
+        else hipLaunchKernelGGL(probe_mfma16_kernel<false>, dim3(cus), dim3(512), 0, s, out, iters);
+    };
+    float ms = 0.0f;
+    int r = probe_time(go, 1, &ms);
+    if (!r) r = TSL_LAUNCHED("probe_mfma16");
+    (void)hipFree(out);
+    if (r) return r;
+    // 32 MFMAs of 16x16x32 (2 x 8192 flops each) per wave per iteration, 8 waves per CU.
+    *tflops = 2.0 * 16 * 16 * 32 * 32 * 8 * (double)cus * iters / (ms * 1e-3) / 1e12;
     return 0;
 }
 
