@@ -1,17 +1,20 @@
-// fp16 GEMMs on CDNA4 matrix cores (v_mfma_f32_32x32x16_f16, f32
-// accumulation): matmul (kernels/matmul.tl:3-17, C = A B with B [K, N]),
-// the llm.tl projections X W^T (linear :28-36, linear_residual :39-47,
-// logits :50-58, gate_up :62-73) and matmul.tl's biased linear (:30-38).
+// fp16 GEMMs on CDNA4 matrix cores (f32 accumulation): matmul
+// (kernels/matmul.tl:3-17, C = A B with B [K, N]), the llm.tl projections
+// X W^T (linear :28-36, linear_residual :39-47, logits :50-58, gate_up
+// :62-73) and matmul.tl's biased linear (:30-38).
 //
 // One workgroup computes a BM x BN tile of C. Each K step of BK stages the
 // A tile and the B tile in LDS as rows of BK contiguous k values (the
 // layout both MFMA operands read: 8 consecutive k per lane), XOR-swizzled
-// by 16-byte chunk so that the 32 rows an MFMA operand read touches fall in
+// by 16-byte chunk so that the rows an MFMA operand read touches fall in
 // distinct banks, and double-buffered: the next tile's global loads are in
-// flight while the current one feeds the MFMAs. B given [K, N] (matmul) is
-// transposed 8x8 in registers on its way to LDS; W given [N, K] is copied.
-// Out-of-range rows and k read as zero and out-of-range outputs are
-// dropped, which is the interpreter's rule (src/interp.rs:93-117, :296-313).
+// flight while the current one feeds the MFMAs. The tiled kernels
+// (gemm_pp16, gemm_big, the skinny forms) issue v_mfma_f32_16x16x32_f16,
+// which the matrix cores sustain at a higher clock on random data than
+// v_mfma_f32_32x32x16_f16; gemm_f16 (any shape and alignment) keeps the
+// 32x32x16 form and stages through registers. Out-of-range rows and k read
+// as zero and out-of-range outputs are dropped, which is the interpreter's
+// rule (src/interp.rs:93-117, :296-313).
 #include "common.h"
 
 #include <algorithm>
