@@ -479,6 +479,28 @@ def test_softmax(rows, cols, bc):
     assert np.abs(got - want).max() <= 1e-6
 
 
+def test_softmax_special_values():
+    # Whole 4096-column rows (the per-chunk form): -inf over every chunk of
+    # some lanes and at the row's end, a row of -inf, +inf and NaN entries,
+    # against the oracle (NaN positions included).
+    _say("softmax special values")
+    r = oracle.Rng(5)
+    x = r.tensor("f32", [8, 4096], 4.0)
+    x[1, :1024] = -np.inf
+    x[2, 3000:] = -np.inf
+    x[3, :] = -np.inf
+    x[4, 17] = np.inf
+    x[5, 4000] = np.nan
+    x[6, ::2] = -np.inf
+    x[7, :] = -1e30
+    x[7, 5] = -1e29
+    want = oracle.softmax(x, BC=4096, threads=8)
+    got = T.run("basic", "softmax", [x, np.zeros_like(x)], meta=[("BC", 4096)], outputs=[1])[1]
+    parity("softmax special", got, want)
+    ok = ~np.isnan(want)
+    assert np.abs(got[ok] - want[ok]).max() <= 1e-6
+
+
 @pytest.mark.parametrize("rows,cols,bc", [(10, 700, 1024), (4096, 4096, 4096), (5, 9000, 16384), (4, 100, 64)])
 def test_rmsnorm_basic(rows, cols, bc):
     _say("rmsnorm basic", rows, cols, bc)
