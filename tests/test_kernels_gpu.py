@@ -115,6 +115,19 @@ def test_matmul_f32_and_linear_bias():
     parity("linear bias", got, oracle.linear_bias(x, w, bias))
 
 
+@pytest.mark.parametrize("m,k,n", [(3900, 512, 4000), (1000, 1000, 1000)])
+def test_linear_bias_large_tiles_ragged(m, k, n):
+    # matmul.tl's biased linear on the 256 x 256 ping-pong tiles (ragged M
+    # and N) and on the smaller tiled forms, against f64.
+    _say("linear bias large tiles", m, k, n)
+    r = oracle.Rng(901 + m)
+    x, w = r.tensor("f16", [m, k], 1.0), r.tensor("f16", [n, k], 1.0 / np.sqrt(k))
+    bias = r.tensor("f16", [n], 1.0)
+    got = T.run("matmul", "linear", [x, w, bias, np.zeros((m, n), np.float16)], outputs=[3])[3]
+    want = x.astype(np.float64) @ w.astype(np.float64).T + bias.astype(np.float64)
+    parity(f"linear bias {m}x{k}x{n}", got, want)
+
+
 # ---------------------------------------------------------------- llm.tl matmuls
 
 MM_CASES = ["linear", "linear_residual", "logits", "gate_up"]
