@@ -514,7 +514,8 @@ def test_softmax_special_values():
     assert np.abs(got[ok] - want[ok]).max() <= 1e-6
 
 
-@pytest.mark.parametrize("rows,cols,bc", [(10, 700, 1024), (4096, 4096, 4096), (5, 9000, 16384), (4, 100, 64)])
+@pytest.mark.parametrize("rows,cols,bc", [(10, 700, 1024), (4096, 4096, 4096), (5, 9000, 16384), (4, 100, 64),
+                                         (13, 2048, 2048), (6, 4096, 4096)])
 def test_rmsnorm_basic(rows, cols, bc):
     _say("rmsnorm basic", rows, cols, bc)
     r = oracle.Rng(3)
