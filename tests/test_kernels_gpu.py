@@ -481,7 +481,8 @@ def test_decode_attention_indexing_properties(mp):
 
 # ---------------------------------------------------------------- rows
 
-@pytest.mark.parametrize("rows,cols,bc", [(10, 700, 1024), (4096, 4096, 4096), (7, 5000, 8192), (3, 40, 16)])
+@pytest.mark.parametrize("rows,cols,bc", [(10, 700, 1024), (4096, 4096, 4096), (7, 5000, 8192), (3, 40, 16),
+                                         (9, 3000, 4096), (5, 4096, 4096)])
 def test_softmax(rows, cols, bc):
     _say("softmax", rows, cols, bc)
     r = oracle.Rng(2)
