@@ -1747,11 +1747,19 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
     if constexpr (BT && !DUAL) {
         if (aligned && M > 64 && tiles(128, 128) < 256 && tiles(64, 64) >= 256) {
             // X W^T at prefill sizes (the engine's 1024-row qkv, o and down):
-            // 64 x 64 tiles of 4 wavefronts and 3 stages fill every CU without
-            // a K split. 1024 x 2048 x 2048: 23.8 -> 18.7 us; x 5632 (split
-            // 2 + reduce before): 47.4 -> 42.8; 1024 x 2560 x 2048: 23.0 -> 22.1.
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 64, 2, 2, 64, 3, false, true>), dim3(tiles(64, 64)), dim3(256), 0, s, A, B, B2, C,
-                               bias, M, N, K, 4);
+            // 128 x 64 tiles, 8 wavefronts when they make one round of
+            // workgroups (one per CU), else 4 (two fit on a CU). On 16x16x32
+            // MFMAs, against the 64 x 64 tiles of 4 wavefronts chosen on
+            // 32x32x16 (same box): down 1024 x 2048 x 5632 39.3 -> 36.2 us,
+            // o 1024 x 2048 x 2048 17.9 -> 17.5, qkv 1024 x 2560 x 2048 (320
+            // tiles, 4 wavefronts) 20.9 -> 18.7; 128 x 128 and 64 x 128 were
+            // slower.
+            if (tiles(128, 64) <= num_cus())
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 64, 4, 2, 64, 3, false, true>), dim3(tiles(128, 64)), dim3(512), 0, s, A,
+                                   B, B2, C, bias, M, N, K, 4);
+            else
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 64, 2, 2, 64, 3, false, true>), dim3(tiles(128, 64)), dim3(256), 0, s, A,
+                                   B, B2, C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
     }
