@@ -287,42 +287,6 @@ TSL_DEV half4 lds_read_tr(const u16* p) {
     return __builtin_bit_cast(half4, v);
 }
 
-// The epilogue of one 32x32 accumulator tile (lane l: column col = .. + l % 32,
-// register r: row row0 + 8 (r / 4) + 4 (l / 32) + r % 4) for the plain
-// epilogues: f16, f32, R += ., + bias. Rows past M and columns past N are
-// dropped.
-template <int EPI>
-TSL_DEV void store_acc32(void* C, const u16* bias, int M, int N, int row0, int col, int g, const float16v& acc) {
-    if (col >= N) return;
-    // The residual's 16 old values, all loads in flight before any store (the
-    // compiler cannot tell the stores from the loads apart, so an
-    // interleaved read-add-write runs serially).
-    float old[EPI == EPI_RESID ? 16 : 1];
-    if constexpr (EPI == EPI_RESID) {
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int row = row0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            old[r] = row < M ? reinterpret_cast<const float*>(C)[(size_t)row * N + col] : 0.0f;
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int row = row0 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (row >= M) continue;
-        const size_t o = (size_t)row * N + col;
-        const float v = acc[r];
-        if constexpr (EPI == EPI_F16) {
-            reinterpret_cast<u16*>(C)[o] = f2h(v);
-        } else if constexpr (EPI == EPI_F32) {
-            reinterpret_cast<float*>(C)[o] = v;
-        } else if constexpr (EPI == EPI_RESID) {
-            reinterpret_cast<float*>(C)[o] = old[r] + v;
-        } else if constexpr (EPI == EPI_BIAS) {
-            reinterpret_cast<u16*>(C)[o] = f2h(v + h2f(bias[col]));
-        }
-    }
-}
-
 // The epilogue of one 16x16 accumulator tile (lane l: column col = .. + l % 16,
 // register r: row row0 + 4 (l / 16) + r) for the plain epilogues.
 template <int EPI>
@@ -355,20 +319,21 @@ TSL_DEV void store_acc16(void* C, const u16* bias, int M, int N, int row0, int c
 }
 
 // The compute of a K step is software pipelined: the MFMA operands of
-// k-step s+1 are read from LDS while the 16 MFMAs of step s run.
+// 32-k substep s+1 are read from LDS while the MFMAs of substep s run.
 //
 // LDS is served 16 lanes per cycle for 16-byte reads and 32 lanes for 8-byte
 // ones, so the swizzles keep every such lane group on distinct banks: A row r
 // holds logical chunk c at chunk c ^ ((r >> 1) & 7) (16 consecutive rows of an
 // operand read cover all 16 slots of the 256-byte bank window); B row k (NN)
-// holds logical chunk c at c ^ ((k & 3) << 2), so the 4 k rows x 2 column
-// halves a 32-lane transposed read touches are 8 distinct 32-byte granules.
+// holds logical chunk c at c ^ (4 (k & 3) + 2 ((k >> 3) & 1)), so the two
+// 16-lane groups a transposed read serves together (4 k rows each, 8 apart,
+// over the same 16 columns) touch 16 distinct 16-byte slots.
 //
 // With SPLIT, gridDim.y = S slices of K: workgroup (t, ks) runs the ks-th of S
 // slices of the K steps and leaves its f32 sums in part[ks][p][m][n] (p: gate,
 // up) for skinny_reduce, which adds the slices in order and applies the
 // epilogue.
-template <bool BT, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS, bool SPLIT = false, bool M16 = false>
+template <bool BT, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS, bool SPLIT = false>
 __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restrict__ A, const u16* __restrict__ B,
                                                              const u16* __restrict__ B2, void* __restrict__ C,
                                                              const u16* __restrict__ bias, int M, int N, int K,
@@ -377,17 +342,16 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     static_assert((BK == 64 || BK == 32) && NS >= 2 && NS <= 4, "k step and stages");
     constexpr int NW = WGM * WGN;                 // wavefronts: WGM x WGN, each (BM/WGM) x (BN/WGN)
     constexpr int WM = BM / WGM, WN = BN / WGN;
-    // M16 (every launch): v_mfma_f32_16x16x32_f16 on 16 x 16 tiles (lane l: row
-    // / column l % 16, k 8 (l / 16) .. +7 of a 32-k substep; gemm_pp16's layout
-    // and B swizzle), which the matrix cores sustain at a higher clock on
-    // random data (prefill-sized products: down 1024x2048x5632 41.8 -> 39.7 us,
-    // gate_up 1024x5632x2048 50.7 -> 48.6, qkv 21.6 -> 21.1). Else the
-    // v_mfma_f32_32x32x16_f16 form on 32 x 32 tiles (16-k substeps), the
-    // layout the swizzles above describe.
-    constexpr int MT = M16 ? 16 : 32;             // MFMA tile edge
+    // v_mfma_f32_16x16x32_f16 on 16 x 16 tiles (lane l: row / column l % 16,
+    // k 8 (l / 16) .. +7 of a 32-k substep; gemm_pp16's layout and B swizzle),
+    // which the matrix cores sustain at a higher clock on random data than the
+    // v_mfma_f32_32x32x16_f16 form this kernel had (prefill-sized products:
+    // down 1024x2048x5632 41.8 -> 39.7 us, gate_up 1024x5632x2048 50.7 -> 48.6,
+    // qkv 21.6 -> 21.1).
+    constexpr int MT = 16;                        // MFMA tile edge
     constexpr int TM = WM / MT, TN = WN / MT;     // MFMA tiles per wave
-    constexpr int KSUB = M16 ? 32 : 16, NSUB = BK / KSUB;  // k per substep, substeps per K step
-    typedef std::conditional_t<M16, float4v, float16v> AccT;
+    constexpr int KSUB = 32, NSUB = BK / KSUB;    // k per substep, substeps per K step
+    typedef float4v AccT;
     constexpr int LPA = BM * BK / 512 / NW, LPB = BN * BK / 512 / NW;  // 1 KB loads per wave per K step
     constexpr int RPL = 512 / BN;                 // B [K, N] rows per 1 KB load
     constexpr int RPA = 512 / BK;                 // A (W) rows per 1 KB load
@@ -400,7 +364,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     TSL_POISON(lds);
     // Row r of an A (W) tile holds logical 16-byte chunk c at c ^ sw(r).
     auto sw = [](int r) { return KC == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
-    auto bsw = [](int k) { return M16 ? ((k & 3) << 2) | (((k >> 3) & 1) << 1) : (k & 3) << 2; };  // B [K, N] rows
+    auto bsw = [](int k) { return ((k & 3) << 2) | (((k >> 3) & 1) << 1); };  // B [K, N] rows
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -408,7 +372,6 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     int tm, tn;
     tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, (N + BN - 1) / BN, G, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int g = lane >> 5;
     const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
 
     // This wave's LPA + LPB loads per K step (for A, then B), each filling 1 KB of
@@ -486,12 +449,12 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
     // LDS byte addresses of this lane's operands in stage 0: A at k-step s,
     // tile i: a_addr[s] + 4096 i; B (NN) tile j: b_addr[j] + (16 s + 4 h) 512.
     const int l16 = lane & 15, g16 = lane >> 4;
-    const int lr = M16 ? l16 : (lane & 31), kg = M16 ? g16 : g;  // operand row / column in the tile, k group
+    const int lr = l16, kg = g16;  // operand row / column in the tile, k group
     uint32_t a_addr[NSUB], b_addr[TN];
 #pragma unroll
     for (int st = 0; st < NSUB; st++) {
         const int r = wm0 + lr;
-        a_addr[st] = (uint32_t)((r * KC + (((M16 ? 4 : 2) * st + kg) ^ sw(r))) * 16);
+        a_addr[st] = (uint32_t)((r * KC + ((4 * st + kg) ^ sw(r))) * 16);
     }
 #pragma unroll
     for (int j = 0; j < TN; j++) {
@@ -499,9 +462,9 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
             const int r = wn0 + j * MT + lr;
             b_addr[j] = (uint32_t)(BM * BK * 2 + r * KC * 16);
         } else {
-            const int grp = lane >> 4, jj = lane & 15;
-            const int n = M16 ? wn0 + j * 16 + 4 * (jj & 3) : wn0 + j * 32 + 16 * (grp & 1) + 4 * (jj & 3);
-            const int k = (M16 ? 8 * g16 : 8 * g) + (jj >> 2);
+            const int jj = lane & 15;
+            const int n = wn0 + j * 16 + 4 * (jj & 3);
+            const int k = 8 * g16 + (jj >> 2);
             b_addr[j] = (uint32_t)(BM * BK * 2 + k * BN * 2 + ((((n >> 3) ^ bsw(k)) << 3) + (n & 7)) * 2);
         }
     }
@@ -513,7 +476,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         for (int j = 0; j < TN; j++) {
             if constexpr (BT) {
                 const int r = wn0 + j * MT + lr;
-                const int cb = so + b_addr[j] + ((((M16 ? 4 : 2) * st + kg) ^ sw(r)) * 16);
+                const int cb = so + b_addr[j] + (((4 * st + kg) ^ sw(r)) * 16);
                 bv[j] = *reinterpret_cast<const half8*>(ldsc + cb);
                 if constexpr (DUAL) bv2[j] = *reinterpret_cast<const half8*>(ldsc + cb + BB);
             } else {
@@ -535,8 +498,7 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
 #pragma unroll
             for (int j = 0; j < TN; j++) acc2[i][j] = AccT{};
     auto mfma = [](const half8& x, const half8& y, const AccT& c) {
-        if constexpr (M16) return __builtin_amdgcn_mfma_f32_16x16x32_f16(x, y, c, 0, 0, 0);
-        else return __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, c, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(x, y, c, 0, 0, 0);
     };
 
     // NS stages in a ring, NS - 1 k steps in flight: iteration kt waits for
@@ -598,14 +560,13 @@ __global__ __launch_bounds__(WGM* WGN * 64, 1) void gemm_big(const u16* __restri
         for (int j = 0; j < TN; j++) {
             const int row0 = m0 + wm0 + i * MT, col = n0 + wn0 + j * MT + lr;
             if constexpr (!SPLIT && !DUAL) {
-                if constexpr (M16) store_acc16<EPI>(C, bias, M, N, row0, col, g16, acc[i][j]);
-                else store_acc32<EPI>(C, bias, M, N, row0, col, g, acc[i][j]);
+                store_acc16<EPI>(C, bias, M, N, row0, col, g16, acc[i][j]);
                 continue;
             }
             if (col >= N) continue;
 #pragma unroll
-            for (int r = 0; r < (M16 ? 4 : 16); r++) {
-                const int row = M16 ? row0 + 4 * g16 + r : row0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            for (int r = 0; r < 4; r++) {
+                const int row = row0 + 4 * g16 + r;
                 if (row >= M) continue;
                 const size_t o = (size_t)row * N + col;
                 const float v = acc[i][j][r];
@@ -1729,7 +1690,7 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             if (K % 64 == 0)
                 hipLaunchKernelGGL((gemm_pp16<BT, EPI>), dim3(tiles(256, 256)), dim3(512), 0, s, A, B, C, bias, M, N, K, 4);
             else
-                hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4, 64, 2, false, true>), dim3(tiles(256, 256)), dim3(512), 0, s, A,
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 256, 2, 4, 64, 2, false>), dim3(tiles(256, 256)), dim3(512), 0, s, A,
                                    B, B2, C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
@@ -1739,7 +1700,7 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             // 8 wavefronts of 64 x 64 x (gate, up): the 256 x 256 tile's
             // register budget, and half the workgroups of 128 x 128 tiles, so
             // prefill-sized products (M ~ 1024) fill the CUs in one round.
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 128, 4, 2, 64, 2, false, true>), dim3(tiles(256, 128)), dim3(512), 0, s, A, B, B2,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 256, 128, 4, 2, 64, 2, false>), dim3(tiles(256, 128)), dim3(512), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
@@ -1755,10 +1716,10 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
             // tiles, 4 wavefronts) 20.9 -> 18.7; 128 x 128 and 64 x 128 were
             // slower.
             if (tiles(128, 64) <= num_cus())
-                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 64, 4, 2, 64, 3, false, true>), dim3(tiles(128, 64)), dim3(512), 0, s, A,
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 64, 4, 2, 64, 3, false>), dim3(tiles(128, 64)), dim3(512), 0, s, A,
                                    B, B2, C, bias, M, N, K, 4);
             else
-                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 64, 2, 2, 64, 3, false, true>), dim3(tiles(128, 64)), dim3(256), 0, s, A,
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 64, 2, 2, 64, 3, false>), dim3(tiles(128, 64)), dim3(256), 0, s, A,
                                    B, B2, C, bias, M, N, K, 4);
             return TSL_LAUNCHED(what);
         }
@@ -1766,7 +1727,7 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
     if (aligned && M > 64 && (BT || !DUAL)) {
         const int split = part ? big_split(M, N, K) : 1;
         if (split > 1) {  // 128 x 128 tiles over K slices, then the ordered sum
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2, true, true>), dim3(tiles(128, 128), split), dim3(256), 0, s, A,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2, true>), dim3(tiles(128, 128), split), dim3(256), 0, s, A,
                                B, B2, C, bias, M, N, K, 4, part);
             const long mn = (long)M * N;
             hipLaunchKernelGGL(skinny_reduce<EPI>, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part, split, M,
@@ -1780,20 +1741,20 @@ int gemm_dispatch(const u16* A, const u16* B, const u16* B2, void* C, const u16*
                 hipLaunchKernelGGL((gemm_pp16<BT, EPI, 128, 128, 2>), dim3(tiles(128, 128)), dim3(512), 0, s, A, B, C, bias,
                                    M, N, K, 4);
             else
-                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 4, 64, 3, false, true>), dim3(tiles(128, 128)), dim3(512), 0, s, A,
+                hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 4, 64, 3, false>), dim3(tiles(128, 128)), dim3(512), 0, s, A,
                                    B, B2, C, bias, M, N, K, 4);
         } else if (tiles(128, 128) >= 256) {
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2, false, true>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 128, 128, 2, 2, 64, 2, false>), dim3(tiles(128, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
         } else if (!BT && tiles(64, 128) < 256 && tiles(32, 128) >= 256) {
             // matmul with too few 64 x 128 tiles to fill the CUs (1024^3):
             // 32 x 128 tiles, 4 wavefronts of 32 x 32 (9.05 -> 7.95 us).
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 32, 128, 1, 4, 64, 2, false, true>), dim3(tiles(32, 128)), dim3(256), 0, s, A, B, B2,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 32, 128, 1, 4, 64, 2, false>), dim3(tiles(32, 128)), dim3(256), 0, s, A, B, B2,
                                C, bias, M, N, K, 4);
         } else {  // 64 x 128 tiles (4 wavefronts of 64 x 32): twice the workgroups;
                   // X W^T keeps two K steps in flight (matmul's in-register B
                   // transpose does better with one)
-            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 128, 1, 4, 64, BT ? 3 : 2, false, true>), dim3(tiles(64, 128)), dim3(256), 0, s, A,
+            hipLaunchKernelGGL((gemm_big<BT, EPI, 64, 128, 1, 4, 64, BT ? 3 : 2, false>), dim3(tiles(64, 128)), dim3(256), 0, s, A,
                                B, B2, C, bias, M, N, K, 4);
         }
         return TSL_LAUNCHED(what);
@@ -1890,7 +1851,7 @@ int launch_linear_residual_rmsnorm(TslKernel& k, const uint64_t* a, hipStream_t 
     const int bsplit = k.scratch && aligned && M > 64 && tiles256 < 224 ? big_split(M, N, K) : 1;
     if (bsplit > 1 && ncols == N && reduce_rmsnorm_fits(N)) {
         const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
-        hipLaunchKernelGGL((gemm_big<true, EPI_RESID, 128, 128, 2, 2, 64, 2, true, true>), dim3(tiles, bsplit), dim3(256), 0, s,
+        hipLaunchKernelGGL((gemm_big<true, EPI_RESID, 128, 128, 2, 2, 64, 2, true>), dim3(tiles, bsplit), dim3(256), 0, s,
                            P<u16>(a[0]), P<u16>(a[1]), nullptr, R, nullptr, M, N, K, 4,
                            reinterpret_cast<float*>(k.scratch));
         if (int e = TSL_LAUNCHED("linear_residual_rmsnorm")) return e;
