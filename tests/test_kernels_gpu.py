@@ -211,6 +211,19 @@ def test_llm_matmuls_ragged_split_tiles(name, m, k, n):
     parity(f"{name} {m}x{k}x{n}", got, want)
 
 
+@pytest.mark.parametrize("name", ["linear", "linear_residual", "logits"])
+@pytest.mark.parametrize("m,k,n", [(900, 1000, 1500), (1000, 1000, 2050)])
+def test_llm_matmuls_prefill_tiles_ragged(name, m, k, n):
+    # Prefill-sized X W^T on 128 x 64 tiles: one round of workgroups (8
+    # wavefronts, 192 tiles) and more than one (4 wavefronts, 264 tiles), with
+    # ragged M and N and a partial last K step.
+    _say("llm mm prefill tiles", name, m, k, n)
+    r = oracle.Rng(500 + m + n)
+    args, want = _mm_args(r, name, m, k, n, wscale=1.0 / np.sqrt(k))
+    got = T.run("llm", name, args, outputs=[len(args) - 1])[len(args) - 1]
+    parity(f"{name} {m}x{k}x{n}", got, want)
+
+
 def test_split_k_products_repeat_bit_identically():
     # The K-split partials are summed in slice order: repeated launches agree
     # bit for bit.
